@@ -1,0 +1,594 @@
+/*
+ * HIP backend of Dataflow_Handle (COMPUTE_HSA) for gfx950.
+ *
+ * Behaviour follows the CUDA backend it replaces
+ * (reference: src/dataflow_handle/nvidia/src/cuda_dataflow_handle.c:53-918,
+ *  src/dataflow_handle/nvidia/src/cuda_drv.c), on HIP's runtime API:
+ *  - native code: a gfx950 code object loaded with hipModuleLoad; every
+ *    function record is keyed by the op's SHA-256 fingerprint;
+ *  - launch geometry: "<op>_set_launch_config" from a dlopen'ed library;
+ *  - submit_op: hipModuleLaunchKernel with kernelParams = op->op_args, then
+ *    the optional "_finish" kernel of two-pass ops on the same stream;
+ *  - streams: non-blocking, default priority; one timing-free event each.
+ * Fixed relative to the reference: submit_peer_transfer is a device-to-device
+ * copy from src to dest (cuda_dataflow_handle.c:912, cuda_drv.c:540,557), and
+ * the device info reads the per-block thread limit (:689).
+ */
+#include "hip_dataflow_handle.h"
+#include "fingerprint.h"
+
+#define HIP_CHECK_RET(call, ret, ...) do { \
+		hipError_t _e = (call); \
+		if (_e != hipSuccess) { \
+			fprintf(stderr, "Error: %s failed: %s. ", #call, hipGetErrorString(_e)); \
+			fprintf(stderr, __VA_ARGS__); \
+			fprintf(stderr, "\n"); \
+			return ret; \
+		} \
+	} while (0)
+
+static uint64_t hip_op_table_hash_func(void * op_fingerprint, uint64_t table_size) {
+	return fingerprint_to_least_sig64((uint8_t *) op_fingerprint, OP_IDENTIFIER_FINGERPRINT_NUM_BYTES) % table_size;
+}
+
+/* stream_id -1 is the NULL stream; anything else must name a created stream */
+static int resolve_stream(Dataflow_Handle * h, int stream_id, hipStream_t * out, const char * what) {
+	if (stream_id == -1) {
+		*out = NULL;
+		return 0;
+	}
+	if (stream_id < 0 || stream_id >= h->num_streams) {
+		fprintf(stderr, "Error: cannot use stream id %d for %s, device has %d streams. Null stream specified by -1...\n",
+				stream_id, what, h->num_streams);
+		return -1;
+	}
+	*out = ((hipStream_t *) h->streams)[stream_id];
+	return 0;
+}
+
+/* ---------- 0. ops ---------- */
+
+static int hip_register_native_code(Dataflow_Handle * dataflow_handle, char * native_code_filename, char * native_code_config_lib_filename,
+									int num_funcs, Op_Skeleton * func_op_skeletons, char ** func_symbols, char ** func_set_launch_symbols, char ** func_init_symbols) {
+	if (dataflow_handle->num_native_function_libs >= MAX_NATIVE_FUNCTION_LIBS) {
+		fprintf(stderr, "Error: cannot register more than %d native function libs...\n", MAX_NATIVE_FUNCTION_LIBS);
+		return -1;
+	}
+	HIP_CHECK_RET(hipSetDevice(dataflow_handle->device_id), -1, "device %d", dataflow_handle->device_id);
+
+	hipModule_t * module = (hipModule_t *) malloc(sizeof(hipModule_t));
+	if (!module) {
+		fprintf(stderr, "Error: malloc failed to allocate space for module container...\n");
+		return -1;
+	}
+	hipError_t err = hipModuleLoad(module, native_code_filename);
+	if (err != hipSuccess) {
+		fprintf(stderr, "Error: unable to load function lib from path: %s (%s)...\n", native_code_filename, hipGetErrorString(err));
+		free(module);
+		return -1;
+	}
+
+	void * config_lib = dlopen(native_code_config_lib_filename, RTLD_LAZY | RTLD_LOCAL);
+	if (!config_lib) {
+		fprintf(stderr, "Error: could not load function config shared lib with dlopen() from path: %s (%s)\n",
+				native_code_config_lib_filename, dlerror());
+		hipModuleUnload(*module);
+		free(module);
+		return -1;
+	}
+
+	int added = 0;
+	for (int i = 0; i < num_funcs; i++) {
+		char * sym = func_symbols[i];
+		if (!sym) {
+			continue;
+		}
+		if (!func_set_launch_symbols[i]) {
+			fprintf(stderr, "Error: set launch symbol not set for native function %s, but is required for native functions..\n", sym);
+			continue;
+		}
+
+		Hip_Function f;
+		memset(&f, 0, sizeof(f));
+		f.is_native = true;
+
+		err = hipModuleGetFunction(&f.function_handle, *module, sym);
+		if (err != hipSuccess) {
+			fprintf(stderr, "Error: failed to load function #%d with name %s from function lib (%s)...\n", i, sym, hipGetErrorString(err));
+			continue;
+		}
+
+		int max_threads = 0;
+		if (hipFuncGetAttribute(&max_threads, HIP_FUNC_ATTRIBUTE_MAX_THREADS_PER_BLOCK, f.function_handle) != hipSuccess || max_threads <= 0) {
+			max_threads = ((Hip_Device_Info *) dataflow_handle->device_info)->max_threads_per_block;
+		}
+		f.function_config.func_max_threads_per_block = MY_MIN(max_threads, HIP_DEV_UPPER_BOUND_MAX_THREADS_ALL_FUNC);
+		f.function_config.func_max_smem = ((Hip_Device_Info *) dataflow_handle->device_info)->max_smem_per_block;
+
+		if (func_init_symbols && func_init_symbols[i]) {
+			Hip_Set_Func_Attribute init_fn = (Hip_Set_Func_Attribute) dlsym(config_lib, func_init_symbols[i]);
+			if (!init_fn) {
+				fprintf(stderr, "Error: failed to load symbol to initialize function #%d with name %s and attribute setting function as %s...\n",
+						i, sym, func_init_symbols[i]);
+				continue;
+			}
+			if (init_fn(dataflow_handle, &f)) {
+				fprintf(stderr, "Error: failed to set function attributes for function #%d with name %s and attribute setting function as %s\n",
+						i, sym, func_init_symbols[i]);
+				continue;
+			}
+		}
+
+		f.set_launch_config = (Hip_Set_Launch_Config) dlsym(config_lib, func_set_launch_symbols[i]);
+		if (!f.set_launch_config) {
+			fprintf(stderr, "Error: failed to get function pointer to launch config for function #%d with name %s and set_launch_config function name as %s\n",
+					i, sym, func_set_launch_symbols[i]);
+			continue;
+		}
+
+		/* optional second pass: "<sym>_finish" + "<op>_set_finish_launch_config" */
+		char finish_sym[FUNC_SYMBOL_MAX_LEN + 16];
+		snprintf(finish_sym, sizeof(finish_sym), "%s_finish", sym);
+		hipFunction_t finish_fn = NULL;
+		if (hipModuleGetFunction(&finish_fn, *module, finish_sym) == hipSuccess && finish_fn) {
+			const char * suffix = "_set_launch_config";
+			size_t len = strlen(func_set_launch_symbols[i]);
+			size_t slen = strlen(suffix);
+			char finish_cfg[FUNC_SYMBOL_MAX_LEN + 32];
+			if (len <= slen || strcmp(func_set_launch_symbols[i] + len - slen, suffix) != 0) {
+				fprintf(stderr, "Error: launch symbol %s of two-pass function %s does not end in %s...\n", func_set_launch_symbols[i], sym, suffix);
+				continue;
+			}
+			snprintf(finish_cfg, sizeof(finish_cfg), "%.*s_set_finish_launch_config", (int) (len - slen), func_set_launch_symbols[i]);
+			f.set_finish_launch_config = (Hip_Set_Launch_Config) dlsym(config_lib, finish_cfg);
+			if (!f.set_finish_launch_config) {
+				fprintf(stderr, "Error: function %s has a finish kernel but no %s in the config lib...\n", sym, finish_cfg);
+				continue;
+			}
+			f.finish_function_handle = finish_fn;
+		}
+		else {
+			/* clear the sticky "not found" status of the failed lookup */
+			(void) hipGetLastError();
+		}
+
+		memcpy(&f.op_skeleton, &func_op_skeletons[i], sizeof(Op_Skeleton));
+		f.hip_external_func = NULL;
+		f.op_extra = NULL;
+
+		if (insert_table(&dataflow_handle->op_table, f.op_skeleton.identifier.fingerprint, &f)) {
+			fprintf(stderr, "Error: failed to insert op for function #%d with name %s to op table...\n", i, sym);
+			continue;
+		}
+		added++;
+	}
+
+	if (added == 0) {
+		fprintf(stderr, "Error: no functions were added to op table...\n");
+		dlclose(config_lib);
+		hipModuleUnload(*module);
+		free(module);
+		return -1;
+	}
+
+	dataflow_handle->native_function_libs[dataflow_handle->num_native_function_libs++] = module;
+	dataflow_handle->num_ops += added;
+	return added;
+}
+
+static int hip_register_external_code(Dataflow_Handle * dataflow_handle, char * external_code_filename, int num_funcs,
+									Op_Skeleton * func_op_skeletons, char ** func_symbols, char ** func_init_symbols) {
+	void * lib = dlopen(external_code_filename, RTLD_LAZY | RTLD_LOCAL);
+	if (!lib) {
+		fprintf(stderr, "Error: could not open external library with path: %s (%s)\n", external_code_filename, dlerror());
+		return -1;
+	}
+	int added = 0;
+	for (int i = 0; i < num_funcs; i++) {
+		char * sym = func_symbols[i];
+		if (!sym) {
+			continue;
+		}
+		Hip_Function f;
+		memset(&f, 0, sizeof(f));
+		f.hip_external_func = (int (*)(Dataflow_Handle *, int, Op *, void *)) dlsym(lib, sym);
+		if (!f.hip_external_func) {
+			fprintf(stderr, "Error: could not obtain function symbol %s from external lib %s...\n", sym, external_code_filename);
+			continue;
+		}
+		if (func_init_symbols && func_init_symbols[i]) {
+			External_Lib_Func_Init init_fn = (External_Lib_Func_Init) dlsym(lib, func_init_symbols[i]);
+			if (!init_fn) {
+				fprintf(stderr, "Error: could not get ref to initialization function %s, for external function %s\n", func_init_symbols[i], sym);
+				continue;
+			}
+			if (init_fn(dataflow_handle, (void *) &f)) {
+				fprintf(stderr, "Error: initialization function %s, for external function %s returned an error...\n", func_init_symbols[i], sym);
+				continue;
+			}
+		}
+		memcpy(&f.op_skeleton, &func_op_skeletons[i], sizeof(Op_Skeleton));
+		f.is_native = false;
+		if (insert_table(&dataflow_handle->op_table, f.op_skeleton.identifier.fingerprint, &f)) {
+			fprintf(stderr, "Error: failed to insert op for function #%d with name %s to op table...\n", i, sym);
+			continue;
+		}
+		added++;
+	}
+	dataflow_handle->num_ops += added;
+	return added;
+}
+
+/* ---------- 1. compute ---------- */
+
+static int launch(hipFunction_t fn, Hip_Launch_Config * cfg, hipStream_t stream, Op * op) {
+	hipError_t err = hipModuleLaunchKernel(fn, cfg->gridDimX, cfg->gridDimY, cfg->gridDimZ,
+											cfg->blockDimX, cfg->blockDimY, cfg->blockDimZ,
+											cfg->sharedMemBytes, stream, op->op_args, NULL);
+	if (err != hipSuccess) {
+		fprintf(stderr, "Error: unable to launch hip function: %s\n", hipGetErrorString(err));
+		return -1;
+	}
+	return 0;
+}
+
+static int hip_submit_op(Dataflow_Handle * dataflow_handle, Op * op, int stream_id) {
+	const char * nick = op->op_skeleton.header.op_nickname;
+	hipStream_t stream;
+	if (resolve_stream(dataflow_handle, stream_id, &stream, nick)) {
+		return -1;
+	}
+
+	Hip_Function * f = NULL;
+	long ind = find_table(&dataflow_handle->op_table, op->op_skeleton.identifier.fingerprint, false, (void **) &f);
+	if (ind == -1 || !f) {
+		fprintf(stderr, "Error: failed to find op with nickname %s and matching dtypes...\n", nick);
+		return -1;
+	}
+
+	if (f->is_native) {
+		Hip_Launch_Config cfg;
+		memset(&cfg, 0, sizeof(cfg));
+		if (f->set_launch_config(&cfg, dataflow_handle, f, op)) {
+			fprintf(stderr, "Error: failed to correctly set launch config for op with nickname %s...\n", nick);
+			return -1;
+		}
+		/* a zero-sized grid means there is no work (e.g. zero rows) */
+		if (cfg.gridDimX == 0 || cfg.gridDimY == 0 || cfg.gridDimZ == 0) {
+			return 0;
+		}
+		if (launch(f->function_handle, &cfg, stream, op)) {
+			fprintf(stderr, "Error: failed to launch kernel for op with nickname %s...\n", nick);
+			return -1;
+		}
+		if (f->finish_function_handle) {
+			Hip_Launch_Config fcfg;
+			memset(&fcfg, 0, sizeof(fcfg));
+			if (f->set_finish_launch_config(&fcfg, dataflow_handle, f, op)) {
+				fprintf(stderr, "Error: failed to set finish launch config for op with nickname %s...\n", nick);
+				return -1;
+			}
+			if (fcfg.gridDimX && fcfg.gridDimY && fcfg.gridDimZ && launch(f->finish_function_handle, &fcfg, stream, op)) {
+				fprintf(stderr, "Error: failed to launch finish kernel for op with nickname %s...\n", nick);
+				return -1;
+			}
+		}
+		return 0;
+	}
+
+	if (!f->hip_external_func) {
+		fprintf(stderr, "Error: if op is not native it must have a reference to external function (error with op having nickname %s)\n", nick);
+		return -1;
+	}
+	if (f->hip_external_func(dataflow_handle, stream_id, op, f->op_extra)) {
+		fprintf(stderr, "Error: failed to do external hip function for op with nickname %s...\n", nick);
+		return -1;
+	}
+	return 0;
+}
+
+static int hip_submit_host_op(Dataflow_Handle * dataflow_handle, void * host_func, void * host_func_arg, int stream_id) {
+	hipStream_t stream;
+	if (resolve_stream(dataflow_handle, stream_id, &stream, "host op")) {
+		return -1;
+	}
+	HIP_CHECK_RET(hipLaunchHostFunc(stream, (hipHostFn_t) host_func, host_func_arg), -1, "failed to launch host function");
+	return 0;
+}
+
+/* ---------- 2. dependencies ---------- */
+
+static void * hip_get_stream_state(Dataflow_Handle * dataflow_handle, int stream_id) {
+	if (stream_id < 0 || stream_id >= dataflow_handle->num_streams) {
+		fprintf(stderr, "Error: cannot get stream state of stream id %d (device has %d streams)...\n", stream_id, dataflow_handle->num_streams);
+		return NULL;
+	}
+	hipStream_t stream = ((hipStream_t *) dataflow_handle->streams)[stream_id];
+	hipEvent_t * events = (hipEvent_t *) dataflow_handle->stream_states;
+	HIP_CHECK_RET(hipEventRecord(events[stream_id], stream), NULL, "failed to record event when trying to get stream state");
+	return &events[stream_id];
+}
+
+static int hip_submit_dependency(Dataflow_Handle * dataflow_handle, int stream_id, void * other_stream_state) {
+	hipStream_t stream;
+	if (!other_stream_state || resolve_stream(dataflow_handle, stream_id, &stream, "dependency")) {
+		return -1;
+	}
+	HIP_CHECK_RET(hipStreamWaitEvent(stream, *((hipEvent_t *) other_stream_state), 0), -1,
+					"failed to have current stream wait on event during submitting dependency");
+	return 0;
+}
+
+static int hip_sync_stream(Dataflow_Handle * dataflow_handle, int stream_id) {
+	hipStream_t stream;
+	if (resolve_stream(dataflow_handle, stream_id, &stream, "sync")) {
+		return -1;
+	}
+	HIP_CHECK_RET(hipStreamSynchronize(stream), -1, "unable to do hip stream synchronize");
+	return 0;
+}
+
+static int hip_sync_handle(Dataflow_Handle * dataflow_handle) {
+	HIP_CHECK_RET(hipSetDevice(dataflow_handle->device_id), -1, "device %d", dataflow_handle->device_id);
+	HIP_CHECK_RET(hipDeviceSynchronize(), -1, "was unable to sync ctx id: %d on device id: %d", dataflow_handle->ctx_id, dataflow_handle->device_id);
+	return 0;
+}
+
+/* ---------- 3. memory ---------- */
+
+static void * hip_alloc_mem(Dataflow_Handle * dataflow_handle, uint64_t size_bytes) {
+	void * p = NULL;
+	HIP_CHECK_RET(hipSetDevice(dataflow_handle->device_id), NULL, "device %d", dataflow_handle->device_id);
+	HIP_CHECK_RET(hipMalloc(&p, (size_t) size_bytes), NULL, "failed to alloc memory on device id %d of size %lu bytes",
+					dataflow_handle->device_id, (unsigned long) size_bytes);
+	return p;
+}
+
+static void hip_free_mem(Dataflow_Handle * dataflow_handle, void * dev_ptr) {
+	if (hipSetDevice(dataflow_handle->device_id) != hipSuccess || hipFree(dev_ptr) != hipSuccess) {
+		fprintf(stderr, "Error: was unable to free memory on device id %d with ptr %p...\n", dataflow_handle->device_id, dev_ptr);
+	}
+}
+
+static int hip_set_mem(Dataflow_Handle * dataflow_handle, int stream_id, void * dev_ptr, uint8_t val, uint64_t size_bytes) {
+	if (stream_id == -1) {
+		HIP_CHECK_RET(hipSetDevice(dataflow_handle->device_id), -1, "device %d", dataflow_handle->device_id);
+		HIP_CHECK_RET(hipMemset(dev_ptr, val, (size_t) size_bytes), -1, "was unable to set memory for device ptr of %p of %lu bytes",
+						dev_ptr, (unsigned long) size_bytes);
+		return 0;
+	}
+	hipStream_t stream;
+	if (resolve_stream(dataflow_handle, stream_id, &stream, "set mem")) {
+		return -1;
+	}
+	HIP_CHECK_RET(hipMemsetAsync(dev_ptr, val, (size_t) size_bytes, stream), -1, "was unable to set memory for device ptr of %p of %lu bytes",
+					dev_ptr, (unsigned long) size_bytes);
+	return 0;
+}
+
+static int hip_enable_access_to_host_mem(Dataflow_Handle * dataflow_handle, void * host_ptr, uint64_t size_bytes, unsigned int flags) {
+	HIP_CHECK_RET(hipHostRegister(host_ptr, (size_t) size_bytes, flags), -1,
+					"failed to enable device id %d to access host memory with ptr %p of size %lu and flags %u",
+					dataflow_handle->device_id, host_ptr, (unsigned long) size_bytes, flags);
+	return 0;
+}
+
+static int hip_disable_access_to_host_mem(Dataflow_Handle * dataflow_handle, void * host_ptr) {
+	HIP_CHECK_RET(hipHostUnregister(host_ptr), -1, "failed to disable host memory access with ptr %p from device id %d",
+					host_ptr, dataflow_handle->device_id);
+	return 0;
+}
+
+static int hip_enable_access_to_peer_mem(Dataflow_Handle * dataflow_handle, Dataflow_Handle * peer_dataflow_handle) {
+	if (peer_dataflow_handle->compute_type != dataflow_handle->compute_type) {
+		fprintf(stderr, "Error: cannot enable peer access, must be same compute type...\n");
+		return -1;
+	}
+	HIP_CHECK_RET(hipSetDevice(dataflow_handle->device_id), -1, "device %d", dataflow_handle->device_id);
+	HIP_CHECK_RET(hipDeviceEnablePeerAccess(peer_dataflow_handle->device_id, 0), -1,
+					"was unable to allow this device (id %d) to access memory on peer device (id %d)",
+					dataflow_handle->device_id, peer_dataflow_handle->device_id);
+	return 0;
+}
+
+static int hip_disable_access_to_peer_mem(Dataflow_Handle * dataflow_handle, Dataflow_Handle * peer_dataflow_handle) {
+	if (peer_dataflow_handle->compute_type != dataflow_handle->compute_type) {
+		fprintf(stderr, "Error: cannot disable peer access, must be same compute type...\n");
+		return -1;
+	}
+	HIP_CHECK_RET(hipSetDevice(dataflow_handle->device_id), -1, "device %d", dataflow_handle->device_id);
+	HIP_CHECK_RET(hipDeviceDisablePeerAccess(peer_dataflow_handle->device_id), -1,
+					"was unable to disable this device (id %d) from accessing memory on peer device (id %d)",
+					dataflow_handle->device_id, peer_dataflow_handle->device_id);
+	return 0;
+}
+
+/* ---------- 4. transfers ---------- */
+
+static int transfer(Dataflow_Handle * h, int stream_id, void * dst, const void * src, uint64_t n, hipMemcpyKind kind, const char * what) {
+	if (stream_id == -1) {
+		HIP_CHECK_RET(hipSetDevice(h->device_id), -1, "device %d", h->device_id);
+		HIP_CHECK_RET(hipMemcpy(dst, src, (size_t) n, kind), -1, "%s of %lu bytes", what, (unsigned long) n);
+		return 0;
+	}
+	hipStream_t stream;
+	if (resolve_stream(h, stream_id, &stream, what)) {
+		return -1;
+	}
+	HIP_CHECK_RET(hipMemcpyAsync(dst, src, (size_t) n, kind, stream), -1, "%s of %lu bytes", what, (unsigned long) n);
+	return 0;
+}
+
+static int hip_submit_inbound_transfer(Dataflow_Handle * dataflow_handle, int stream_id, void * dev_dest, void * host_src, uint64_t size_bytes) {
+	return transfer(dataflow_handle, stream_id, dev_dest, host_src, size_bytes, hipMemcpyHostToDevice, "inbound transfer");
+}
+
+static int hip_submit_outbound_transfer(Dataflow_Handle * dataflow_handle, int stream_id, void * host_dest, void * dev_src, uint64_t size_bytes) {
+	return transfer(dataflow_handle, stream_id, host_dest, dev_src, size_bytes, hipMemcpyDeviceToHost, "outbound transfer");
+}
+
+static int hip_submit_peer_transfer(Dataflow_Handle * dataflow_handle, int stream_id, void * dev_dest, void * dev_src, uint64_t size_bytes) {
+	return transfer(dataflow_handle, stream_id, dev_dest, dev_src, size_bytes, hipMemcpyDeviceToDevice, "peer transfer");
+}
+
+/* ---------- init / destroy ---------- */
+
+static int hip_set_device_info(Hip_Device_Info * info, int device_id) {
+	hipDeviceProp_t prop;
+	HIP_CHECK_RET(hipGetDeviceProperties(&prop, device_id), -1, "device %d", device_id);
+	memset(info, 0, sizeof(*info));
+	info->total_mem = prop.totalGlobalMem;
+	info->cu_count = prop.multiProcessorCount;
+	info->max_threads_per_block = MY_MIN(prop.maxThreadsPerBlock, HIP_DEV_UPPER_BOUND_MAX_THREADS_ALL_FUNC);
+	info->max_smem_per_block = (int) prop.sharedMemPerBlock;
+	info->optin_max_smem_per_block = (int) prop.sharedMemPerBlock;
+	info->warp_size = prop.warpSize;
+	info->l2_bytes = prop.l2CacheSize;
+	strncpy(info->arch_name, prop.gcnArchName, sizeof(info->arch_name) - 1);
+	info->arch_name[sizeof(info->arch_name) - 1] = '\0';
+	/* "gfx950:sramecc+:xnack-" -> 950 (hex digits in the stepping, e.g. 90a, keep decimal prefix) */
+	info->arch_num = 0;
+	if (strncmp(prop.gcnArchName, "gfx", 3) == 0) {
+		info->arch_num = (int) strtol(prop.gcnArchName + 3, NULL, 10);
+	}
+	int v = 0;
+	info->num_xcds = (hipDeviceGetAttribute(&v, hipDeviceAttributeNumberOfXccs, device_id) == hipSuccess && v > 0) ? v : 1;
+	v = -1;
+	info->host_numa_id = (hipDeviceGetAttribute(&v, hipDeviceAttributeHostNumaId, device_id) == hipSuccess) ? v : -1;
+	(void) hipGetLastError();
+	return 0;
+}
+
+int init_hip_dataflow_handle(Dataflow_Handle * dataflow_handle, ComputeType compute_type, int device_id,
+								int ctx_id, unsigned int ctx_flags,
+								int num_streams, int * opt_stream_prios, char ** opt_stream_names) {
+	(void) ctx_flags;
+	if (num_streams < 0 || num_streams > MAX_STREAMS) {
+		fprintf(stderr, "Error: num_streams must be in [0, %d], got %d...\n", MAX_STREAMS, num_streams);
+		return -1;
+	}
+	memset(dataflow_handle, 0, sizeof(*dataflow_handle));
+	dataflow_handle->compute_type = compute_type;
+	dataflow_handle->device_id = device_id;
+	dataflow_handle->ctx_id = ctx_id;
+
+	int count = 0;
+	HIP_CHECK_RET(hipGetDeviceCount(&count), -1, "failed to initialize the hip runtime");
+	if (device_id < 0 || device_id >= count) {
+		fprintf(stderr, "Error: failed to get device handle for dev id: %d (%d devices)...\n", device_id, count);
+		return -1;
+	}
+	HIP_CHECK_RET(hipSetDevice(device_id), -1, "device %d", device_id);
+
+	dataflow_handle->device_handle = malloc(sizeof(int));
+	dataflow_handle->device_info = malloc(sizeof(Hip_Device_Info));
+	dataflow_handle->ctx = malloc(sizeof(int));
+	if (!dataflow_handle->device_handle || !dataflow_handle->device_info || !dataflow_handle->ctx) {
+		fprintf(stderr, "Error: malloc failed while creating the handle...\n");
+		return -1;
+	}
+	*((int *) dataflow_handle->device_handle) = device_id;
+	*((int *) dataflow_handle->ctx) = device_id;
+	if (hip_set_device_info((Hip_Device_Info *) dataflow_handle->device_info, device_id)) {
+		fprintf(stderr, "Error: was unable to set hip device info for dev id: %d...\n", device_id);
+		return -1;
+	}
+
+	dataflow_handle->num_streams = num_streams;
+	bool warned = false;
+	for (int i = 0; i < MAX_STREAMS; i++) {
+		dataflow_handle->stream_prios[i] = (i < num_streams) ? (opt_stream_prios ? opt_stream_prios[i] : HIP_DEFAULT_STREAM_PRIO) : -1;
+		if (i < num_streams && dataflow_handle->stream_prios[i] != HIP_DEFAULT_STREAM_PRIO && !warned) {
+			fprintf(stderr, "Warning: stream priorities are recorded but every stream is created at the default priority...\n");
+			warned = true;
+		}
+		dataflow_handle->stream_names[i] = NULL;
+		if (i < num_streams && opt_stream_names && opt_stream_names[i]) {
+			dataflow_handle->stream_names[i] = strdup(opt_stream_names[i]);
+			if (!dataflow_handle->stream_names[i]) {
+				fprintf(stderr, "Error: failed to alloc space to hold stream name...\n");
+				return -1;
+			}
+		}
+	}
+
+	size_t ns = (size_t) (num_streams > 0 ? num_streams : 1);
+	dataflow_handle->streams = calloc(ns, sizeof(hipStream_t));
+	dataflow_handle->stream_states = calloc(ns, sizeof(hipEvent_t));
+	if (!dataflow_handle->streams || !dataflow_handle->stream_states) {
+		fprintf(stderr, "Error: malloc failed to allocate stream containers...\n");
+		return -1;
+	}
+	hipStream_t * streams = (hipStream_t *) dataflow_handle->streams;
+	hipEvent_t * events = (hipEvent_t *) dataflow_handle->stream_states;
+	for (int i = 0; i < num_streams; i++) {
+		HIP_CHECK_RET(hipStreamCreateWithFlags(&streams[i], hipStreamNonBlocking), -1, "unable to initialize stream #%d on device id %d", i, device_id);
+		HIP_CHECK_RET(hipEventCreateWithFlags(&events[i], hipEventDisableTiming), -1, "unable to initialize event for stream #%d on device id %d", i, device_id);
+	}
+
+	dataflow_handle->num_native_function_libs = 0;
+	dataflow_handle->num_ops = 0;
+	if (init_table(&dataflow_handle->op_table, hip_op_table_hash_func, OP_IDENTIFIER_FINGERPRINT_NUM_BYTES, sizeof(Hip_Function),
+					OP_TABLE_MIN_SIZE, OP_TABLE_MAX_SIZE, 1.0f, 1.0f)) {
+		fprintf(stderr, "Error: failed to init op table...\n");
+		return -1;
+	}
+
+	dataflow_handle->register_native_code = hip_register_native_code;
+	dataflow_handle->register_external_code = hip_register_external_code;
+	dataflow_handle->submit_op = hip_submit_op;
+	dataflow_handle->submit_host_op = hip_submit_host_op;
+	dataflow_handle->get_stream_state = hip_get_stream_state;
+	dataflow_handle->submit_dependency = hip_submit_dependency;
+	dataflow_handle->sync_stream = hip_sync_stream;
+	dataflow_handle->sync_handle = hip_sync_handle;
+	dataflow_handle->alloc_mem = hip_alloc_mem;
+	dataflow_handle->free_mem = hip_free_mem;
+	dataflow_handle->set_mem = hip_set_mem;
+	dataflow_handle->enable_access_to_host_mem = hip_enable_access_to_host_mem;
+	dataflow_handle->disable_access_to_host_mem = hip_disable_access_to_host_mem;
+	dataflow_handle->enable_access_to_peer_mem = hip_enable_access_to_peer_mem;
+	dataflow_handle->disable_access_to_peer_mem = hip_disable_access_to_peer_mem;
+	dataflow_handle->submit_inbound_transfer = hip_submit_inbound_transfer;
+	dataflow_handle->submit_outbound_transfer = hip_submit_outbound_transfer;
+	dataflow_handle->submit_peer_transfer = hip_submit_peer_transfer;
+	return 0;
+}
+
+int destroy_hip_dataflow_handle(Dataflow_Handle * dataflow_handle) {
+	int ret = 0;
+	if (hipSetDevice(dataflow_handle->device_id) != hipSuccess || hipDeviceSynchronize() != hipSuccess) {
+		ret = -1;
+	}
+	hipStream_t * streams = (hipStream_t *) dataflow_handle->streams;
+	hipEvent_t * events = (hipEvent_t *) dataflow_handle->stream_states;
+	for (int i = 0; i < dataflow_handle->num_streams; i++) {
+		if (events && events[i]) hipEventDestroy(events[i]);
+		if (streams && streams[i]) hipStreamDestroy(streams[i]);
+		free(dataflow_handle->stream_names[i]);
+		dataflow_handle->stream_names[i] = NULL;
+	}
+	for (int i = 0; i < dataflow_handle->num_native_function_libs; i++) {
+		hipModule_t * m = (hipModule_t *) dataflow_handle->native_function_libs[i];
+		if (m) {
+			hipModuleUnload(*m);
+			free(m);
+		}
+		dataflow_handle->native_function_libs[i] = NULL;
+	}
+	dataflow_handle->num_native_function_libs = 0;
+	destroy_table(&dataflow_handle->op_table);
+	free(dataflow_handle->streams);
+	free(dataflow_handle->stream_states);
+	free(dataflow_handle->device_handle);
+	free(dataflow_handle->device_info);
+	free(dataflow_handle->ctx);
+	dataflow_handle->streams = NULL;
+	dataflow_handle->stream_states = NULL;
+	dataflow_handle->device_handle = NULL;
+	dataflow_handle->device_info = NULL;
+	dataflow_handle->ctx = NULL;
+	dataflow_handle->num_streams = 0;
+	dataflow_handle->num_ops = 0;
+	return ret;
+}

@@ -1,0 +1,248 @@
+/*
+ * Launch geometry of the gfx950 kernels (dlopen'ed by the HIP backend).
+ * One "<op>_set_launch_config" per op family, as the reference's
+ * src/ops/nvidia/{norm/rms_norm_config.c, attention/attn_misc_config.c,
+ * activations/swiglu_config.c, loss/loss_misc_config.c}; the geometry itself is
+ * chosen for CDNA (wave64, CU count, LDS) and shared with the kernels through
+ * kernel_geometry.h. Every function validates the arguments the kernel relies
+ * on and returns -1 with a message instead of launching out of range.
+ */
+#include "hip_ops_config.h"
+#include "kernel_geometry.h"
+
+#define ARG(op, i, type) (*((type *) (op)->op_args[(i)]))
+
+static void set_1d(Hip_Launch_Config * c, unsigned grid, unsigned block, unsigned lds) {
+	c->gridDimX = grid;
+	c->gridDimY = 1;
+	c->gridDimZ = 1;
+	c->blockDimX = block;
+	c->blockDimY = 1;
+	c->blockDimZ = 1;
+	c->sharedMemBytes = lds;
+}
+
+static const Hip_Device_Info * dev(Dataflow_Handle * h) { return (const Hip_Device_Info *) h->device_info; }
+
+static size_t arg_elem_bytes(Hip_Function * f, int i) {
+	return dataflow_sizeof_element(f->op_skeleton.header.arg_dtypes[i]);
+}
+
+static unsigned long long ptr_bits(const void * p) { return (unsigned long long) (uintptr_t) p; }
+
+/* ---------------- RMSNorm ---------------- */
+
+int rms_norm_set_attribute_config(Dataflow_Handle * dataflow_handle, Hip_Function * hip_function) {
+	/* LDS needs no opt-in on CDNA: every function may use the per-workgroup maximum */
+	hip_function->function_config.func_max_smem = dev(dataflow_handle)->max_smem_per_block;
+	int max_threads = 0;
+	if (hipFuncGetAttribute(&max_threads, HIP_FUNC_ATTRIBUTE_MAX_THREADS_PER_BLOCK, hip_function->function_handle) != hipSuccess) {
+		fprintf(stderr, "Error: could not get rms norm attribute for max_threads_per_block...\n");
+		return -1;
+	}
+	hip_function->function_config.func_max_threads_per_block = max_threads;
+	return 0;
+}
+
+static int rms_check(const char * what, int n_rows, int n_cols, size_t elem) {
+	if (n_rows < 0 || n_cols < 0 || elem == 0) {
+		fprintf(stderr, "Error: %s: invalid shape (%d x %d) or dtype...\n", what, n_rows, n_cols);
+		return -1;
+	}
+	return 0;
+}
+
+/* rows per workgroup-iteration and grid for the row-streaming ops */
+static void rms_rowwise(Hip_Launch_Config * c, Dataflow_Handle * h, int n_rows, int nv) {
+	const int tpr = rms_tpr_for(nv);
+	const int per_cu = MY_MAX(1, 2048 / tpr);   /* ~32 waves of row slots per CU */
+	long grid = MY_MIN((long) n_rows, (long) dev(h)->cu_count * per_cu);
+	set_1d(c, (unsigned) grid, (unsigned) tpr, (unsigned) (RMS_CELLS_PER_SLOT * sizeof(float)));
+}
+
+int rms_norm_set_launch_config(Hip_Launch_Config * hip_launch_config, Dataflow_Handle * dataflow_handle, Hip_Function * hip_function, Op * op) {
+	const int n_rows = ARG(op, 0, int), n_cols = ARG(op, 1, int);
+	const size_t elem = arg_elem_bytes(hip_function, 3);
+	if (rms_check("rms norm", n_rows, n_cols, elem)) return -1;
+	const int nv = rms_vec_chunks(n_cols, (int) elem, ptr_bits(ARG(op, 3, void *)) | ptr_bits(ARG(op, 4, void *)) | ptr_bits(ARG(op, 5, void *)));
+	rms_rowwise(hip_launch_config, dataflow_handle, (n_cols == 0) ? 0 : n_rows, nv);
+	return 0;
+}
+
+int rms_norm_bwd_x_set_launch_config(Hip_Launch_Config * hip_launch_config, Dataflow_Handle * dataflow_handle, Hip_Function * hip_function, Op * op) {
+	const int n_rows = ARG(op, 0, int), n_cols = ARG(op, 1, int);
+	const size_t elem = arg_elem_bytes(hip_function, 5);
+	if (rms_check("rms norm bwd x", n_rows, n_cols, elem)) return -1;
+	const int nv = rms_vec_chunks(n_cols, (int) elem, ptr_bits(ARG(op, 5, void *)) | ptr_bits(ARG(op, 6, void *)) |
+													ptr_bits(ARG(op, 7, void *)) | ptr_bits(ARG(op, 8, void *)));
+	rms_rowwise(hip_launch_config, dataflow_handle, (n_cols == 0) ? 0 : n_rows, nv);
+	return 0;
+}
+
+/* two-pass dW ops: pick slots and grid so LDS and the partial scratch fit */
+static int rms_dw_config(Hip_Launch_Config * c, Dataflow_Handle * h, Hip_Function * f, const char * what, int n_rows, int n_cols, int nv) {
+	if (n_rows == 0 || n_cols == 0) {
+		set_1d(c, 0, 1, 0);
+		return 0;
+	}
+	const int tpr = rms_tpr_for(nv);
+	const long max_lds = f->function_config.func_max_smem > 0 ? f->function_config.func_max_smem : dev(h)->max_smem_per_block;
+	int slots = MY_MAX(1, RMS_MAX_TPR / tpr);
+	long lds = 0;
+	for (; slots >= 1; slots--) {
+		const long colbuf = (nv > 0) ? (long) n_cols : (long) slots * n_cols;
+		lds = (long) (RMS_CELLS_PER_SLOT * slots + colbuf) * (long) sizeof(float);
+		if (lds <= max_lds) break;
+	}
+	if (slots < 1) {
+		fprintf(stderr, "Error: %s: rows of %d columns need more LDS than the %ld bytes available...\n", what, n_cols, max_lds);
+		return -1;
+	}
+	const long max_parts = (long) RMS_DW_SCRATCH_FLOATS / (long) n_cols;
+	if (max_parts < 1) {
+		fprintf(stderr, "Error: %s: %d columns exceed the dW scratch of %u floats...\n", what, n_cols, (unsigned) RMS_DW_SCRATCH_FLOATS);
+		return -1;
+	}
+	long grid = MY_MIN((long) MY_CEIL((long) n_rows, (long) slots), (long) dev(h)->cu_count);
+	grid = MY_MIN(grid, max_parts);
+	set_1d(c, (unsigned) grid, (unsigned) (slots * tpr), (unsigned) lds);
+	return 0;
+}
+
+static int rms_dw_finish_config(Hip_Launch_Config * c, int n_rows, int n_cols) {
+	if (n_rows == 0 || n_cols == 0) {
+		set_1d(c, 0, 1, 0);
+		return 0;
+	}
+	set_1d(c, (unsigned) MY_CEIL(n_cols, 256), 256, 0);
+	return 0;
+}
+
+int rms_norm_bwd_w_set_launch_config(Hip_Launch_Config * hip_launch_config, Dataflow_Handle * dataflow_handle, Hip_Function * hip_function, Op * op) {
+	const int n_rows = ARG(op, 0, int), n_cols = ARG(op, 1, int);
+	const size_t elem = arg_elem_bytes(hip_function, 4);
+	if (rms_check("rms norm bwd w", n_rows, n_cols, elem)) return -1;
+	const int nv = rms_vec_chunks(n_cols, (int) elem, ptr_bits(ARG(op, 4, void *)) | ptr_bits(ARG(op, 5, void *)));
+	return rms_dw_config(hip_launch_config, dataflow_handle, hip_function, "rms norm bwd w", n_rows, n_cols, nv);
+}
+
+int rms_norm_bwd_w_set_finish_launch_config(Hip_Launch_Config * hip_launch_config, Dataflow_Handle * dataflow_handle, Hip_Function * hip_function, Op * op) {
+	(void) dataflow_handle;
+	(void) hip_function;
+	return rms_dw_finish_config(hip_launch_config, ARG(op, 0, int), ARG(op, 1, int));
+}
+
+int rms_norm_bwd_set_launch_config(Hip_Launch_Config * hip_launch_config, Dataflow_Handle * dataflow_handle, Hip_Function * hip_function, Op * op) {
+	const int n_rows = ARG(op, 0, int), n_cols = ARG(op, 1, int);
+	const size_t elem = arg_elem_bytes(hip_function, 5);
+	if (rms_check("rms norm bwd", n_rows, n_cols, elem)) return -1;
+	const int nv = rms_vec_chunks(n_cols, (int) elem, ptr_bits(ARG(op, 4, void *)) | ptr_bits(ARG(op, 5, void *)) |
+													ptr_bits(ARG(op, 6, void *)) | ptr_bits(ARG(op, 7, void *)));
+	return rms_dw_config(hip_launch_config, dataflow_handle, hip_function, "rms norm bwd", n_rows, n_cols, nv);
+}
+
+int rms_norm_bwd_set_finish_launch_config(Hip_Launch_Config * hip_launch_config, Dataflow_Handle * dataflow_handle, Hip_Function * hip_function, Op * op) {
+	(void) dataflow_handle;
+	(void) hip_function;
+	return rms_dw_finish_config(hip_launch_config, ARG(op, 0, int), ARG(op, 1, int));
+}
+
+/* ---------------- RoPE ---------------- */
+
+static int rope_config(Hip_Launch_Config * c, Dataflow_Handle * h, Op * op, const char * what) {
+	const uint64_t N = ARG(op, 0, uint64_t);
+	const int model_dim = ARG(op, 1, int), head_dim = ARG(op, 2, int), num_kv_heads = ARG(op, 3, int);
+	if (model_dim <= 0 || head_dim <= 0 || (head_dim & 1) || head_dim > ROPE_MAX_HEAD_DIM || (model_dim % head_dim) != 0 ||
+		num_kv_heads < 0 || (N % (uint64_t) model_dim) != 0) {
+		fprintf(stderr, "Error: %s: unsupported shape N=%lu model_dim=%d head_dim=%d num_kv_heads=%d "
+				"(need even head_dim <= %d dividing model_dim, and N a multiple of model_dim)...\n",
+				what, (unsigned long) N, model_dim, head_dim, num_kv_heads, ROPE_MAX_HEAD_DIM);
+		return -1;
+	}
+	const uint64_t n_tokens = N / (uint64_t) model_dim;
+	uint64_t grid = MY_CEIL(n_tokens, (uint64_t) ROPE_WAVES);
+	grid = MY_MIN(grid, (uint64_t) dev(h)->cu_count * 8u);
+	set_1d(c, (unsigned) grid, 64 * ROPE_WAVES, 0);
+	return 0;
+}
+
+int rope_set_launch_config(Hip_Launch_Config * hip_launch_config, Dataflow_Handle * dataflow_handle, Hip_Function * hip_function, Op * op) {
+	(void) hip_function;
+	return rope_config(hip_launch_config, dataflow_handle, op, "rope");
+}
+
+int rope_bwd_x_set_launch_config(Hip_Launch_Config * hip_launch_config, Dataflow_Handle * dataflow_handle, Hip_Function * hip_function, Op * op) {
+	(void) hip_function;
+	return rope_config(hip_launch_config, dataflow_handle, op, "rope bwd x");
+}
+
+/* ---------------- SwiGLU ---------------- */
+
+static int swiglu_config(Hip_Launch_Config * c, Dataflow_Handle * h, Hip_Function * f, Op * op, const char * what) {
+	const int rows = ARG(op, 0, int), cols = ARG(op, 1, int);
+	const size_t elem = arg_elem_bytes(f, 2);
+	if (rows < 0 || cols < 0 || elem == 0) {
+		fprintf(stderr, "Error: %s: invalid shape (%d x %d) or dtype...\n", what, rows, cols);
+		return -1;
+	}
+	const long n = (long) rows * (long) cols;
+	const long chunks = MY_CEIL(n, (long) (16 / elem));
+	long grid = MY_CEIL(chunks, 256L * SWIGLU_UNROLL);
+	grid = MY_MIN(grid, (long) dev(h)->cu_count * 16L);
+	set_1d(c, (unsigned) grid, 256, 0);
+	return 0;
+}
+
+int swiglu_set_launch_config(Hip_Launch_Config * hip_launch_config, Dataflow_Handle * dataflow_handle, Hip_Function * hip_function, Op * op) {
+	return swiglu_config(hip_launch_config, dataflow_handle, hip_function, op, "swiglu");
+}
+
+int swiglu_bwd_x_set_launch_config(Hip_Launch_Config * hip_launch_config, Dataflow_Handle * dataflow_handle, Hip_Function * hip_function, Op * op) {
+	return swiglu_config(hip_launch_config, dataflow_handle, hip_function, op, "swiglu bwd x");
+}
+
+/* ---------------- softmax / cross-entropy ---------------- */
+
+/* one workgroup per row; small rows get a smaller workgroup */
+static int smx_config(Hip_Launch_Config * c, Hip_Function * f, int n_rows, int n_cols, const char * what) {
+	const size_t elem = arg_elem_bytes(f, 2);
+	if (n_rows < 0 || n_cols < 0 || elem == 0) {
+		fprintf(stderr, "Error: %s: invalid shape (%d x %d) or dtype...\n", what, n_rows, n_cols);
+		return -1;
+	}
+	if (n_rows == 0 || n_cols == 0) {
+		set_1d(c, 0, 1, 0);
+		return 0;
+	}
+	const long nv = MY_CEIL((long) n_cols, (long) (16 / elem));
+	long block = MY_CEIL(MY_CEIL(nv, (long) SMX_MAXCH), 64L) * 64L;
+	block = MY_MAX(64L, MY_MIN(block, (long) SMX_THREADS));
+	set_1d(c, (unsigned) n_rows, (unsigned) block, 0);
+	return 0;
+}
+
+int softmax_set_launch_config(Hip_Launch_Config * hip_launch_config, Dataflow_Handle * dataflow_handle, Hip_Function * hip_function, Op * op) {
+	(void) dataflow_handle;
+	return smx_config(hip_launch_config, hip_function, ARG(op, 0, int), ARG(op, 1, int), "softmax");
+}
+
+int softmax_cross_entropy_loss_set_launch_config(Hip_Launch_Config * hip_launch_config, Dataflow_Handle * dataflow_handle, Hip_Function * hip_function, Op * op) {
+	(void) dataflow_handle;
+	if (ARG(op, 5, float *) && !ARG(op, 4, float *)) {
+		fprintf(stderr, "Error: softmax cross entropy loss: mean_loss needs the per-row loss buffer...\n");
+		return -1;
+	}
+	return smx_config(hip_launch_config, hip_function, ARG(op, 0, int), ARG(op, 1, int), "softmax cross entropy loss");
+}
+
+int cross_entropy_loss_set_launch_config(Hip_Launch_Config * hip_launch_config, Dataflow_Handle * dataflow_handle, Hip_Function * hip_function, Op * op) {
+	(void) dataflow_handle;
+	(void) hip_function;
+	const int n_rows = ARG(op, 0, int);
+	if (n_rows < 0) {
+		fprintf(stderr, "Error: cross entropy loss: invalid n_rows %d...\n", n_rows);
+		return -1;
+	}
+	set_1d(hip_launch_config, (unsigned) MY_CEIL(n_rows, 256), 256, 0);
+	return 0;
+}

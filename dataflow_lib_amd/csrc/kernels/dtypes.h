@@ -1,0 +1,134 @@
+/*
+ * Storage types and 16-byte vector pack/unpack for the gfx950 kernels.
+ *
+ * Storage: fp32, fp16 (IEEE binary16) and bf16, all row-major. Arithmetic is
+ * always fp32. Narrowing conversions round to nearest even: bf16 pairs use
+ * the gfx950 packed convert (v_cvt_pk_bf16_f32), fp16 the IEEE convert.
+ */
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+struct bf16_t { uint16_t bits; };
+struct f16_t { uint16_t bits; };
+
+typedef __attribute__((ext_vector_type(2))) __bf16 bf16x2_v;
+typedef __attribute__((ext_vector_type(2))) _Float16 f16x2_v;
+
+/* one 16-byte memory vector */
+struct __attribute__((aligned(16))) R16 {
+	uint32_t w[4];
+};
+
+__device__ __forceinline__ float to_f(float x) { return x; }
+__device__ __forceinline__ float to_f(bf16_t x) { return __uint_as_float(((uint32_t) x.bits) << 16); }
+__device__ __forceinline__ float to_f(f16_t x) { return (float) __builtin_bit_cast(_Float16, x.bits); }
+
+template <typename T> __device__ __forceinline__ T from_f(float f);
+template <> __device__ __forceinline__ float from_f<float>(float f) { return f; }
+template <> __device__ __forceinline__ bf16_t from_f<bf16_t>(float f) { return bf16_t{__builtin_bit_cast(uint16_t, (__bf16) f)}; }
+template <> __device__ __forceinline__ f16_t from_f<f16_t>(float f) { return f16_t{__builtin_bit_cast(uint16_t, (_Float16) f)}; }
+
+/* elements per 16-byte vector */
+template <typename T> struct VecOf { static constexpr int N = 16 / (int) sizeof(T); };
+
+/* low / high element of a packed 2 x 16-bit word */
+__device__ __forceinline__ float bf16_lo(uint32_t w) { return __uint_as_float(w << 16); }
+__device__ __forceinline__ float bf16_hi(uint32_t w) { return __uint_as_float(w & 0xffff0000u); }
+
+__device__ __forceinline__ uint32_t pack_bf16x2(float lo, float hi) {
+	bf16x2_v v = {(__bf16) lo, (__bf16) hi};
+	return __builtin_bit_cast(uint32_t, v);
+}
+__device__ __forceinline__ uint32_t pack_f16x2(float lo, float hi) {
+	f16x2_v v = {(_Float16) lo, (_Float16) hi};
+	return __builtin_bit_cast(uint32_t, v);
+}
+
+template <typename T> __device__ __forceinline__ void unpack16(const R16 & r, float * f);
+template <> __device__ __forceinline__ void unpack16<float>(const R16 & r, float * f) {
+#pragma unroll
+	for (int i = 0; i < 4; i++) f[i] = __uint_as_float(r.w[i]);
+}
+template <> __device__ __forceinline__ void unpack16<bf16_t>(const R16 & r, float * f) {
+#pragma unroll
+	for (int i = 0; i < 4; i++) { f[2 * i] = bf16_lo(r.w[i]); f[2 * i + 1] = bf16_hi(r.w[i]); }
+}
+template <> __device__ __forceinline__ void unpack16<f16_t>(const R16 & r, float * f) {
+#pragma unroll
+	for (int i = 0; i < 4; i++) {
+		f16x2_v h = __builtin_bit_cast(f16x2_v, r.w[i]);
+		f[2 * i] = (float) h.x;
+		f[2 * i + 1] = (float) h.y;
+	}
+}
+
+template <typename T> __device__ __forceinline__ R16 pack16(const float * f);
+template <> __device__ __forceinline__ R16 pack16<float>(const float * f) {
+	R16 r;
+#pragma unroll
+	for (int i = 0; i < 4; i++) r.w[i] = __float_as_uint(f[i]);
+	return r;
+}
+template <> __device__ __forceinline__ R16 pack16<bf16_t>(const float * f) {
+	R16 r;
+#pragma unroll
+	for (int i = 0; i < 4; i++) r.w[i] = pack_bf16x2(f[2 * i], f[2 * i + 1]);
+	return r;
+}
+template <> __device__ __forceinline__ R16 pack16<f16_t>(const float * f) {
+	R16 r;
+#pragma unroll
+	for (int i = 0; i < 4; i++) r.w[i] = pack_f16x2(f[2 * i], f[2 * i + 1]);
+	return r;
+}
+
+/*
+ * A "chunk" is V consecutive elements handled by one lane: V = VecOf<T>::N
+ * (one 16-byte access) on the vector path, V = 1 on the element path used
+ * for unaligned or ragged rows. raw_t is what sits in registers.
+ */
+template <typename T, int V> struct Chunk {
+	using raw_t = R16;
+	static_assert(V == VecOf<T>::N, "vector chunk must be 16 bytes");
+	__device__ static __forceinline__ raw_t load(const T * base, long idx) { return reinterpret_cast<const R16 *>(base)[idx]; }
+	__device__ static __forceinline__ void store(T * base, long idx, const raw_t & r) { reinterpret_cast<R16 *>(base)[idx] = r; }
+	__device__ static __forceinline__ void unpack(const raw_t & r, float * f) { unpack16<T>(r, f); }
+	__device__ static __forceinline__ raw_t pack(const float * f) { return pack16<T>(f); }
+	__device__ static __forceinline__ raw_t zero() { R16 r; r.w[0] = r.w[1] = r.w[2] = r.w[3] = 0u; return r; }
+};
+template <typename T> struct Chunk<T, 1> {
+	using raw_t = T;
+	__device__ static __forceinline__ raw_t load(const T * base, long idx) { return base[idx]; }
+	__device__ static __forceinline__ void store(T * base, long idx, const raw_t & r) { base[idx] = r; }
+	__device__ static __forceinline__ void unpack(const raw_t & r, float * f) { f[0] = to_f(r); }
+	__device__ static __forceinline__ raw_t pack(const float * f) { return from_f<T>(f[0]); }
+	__device__ static __forceinline__ raw_t zero() { return from_f<T>(0.0f); }
+};
+
+__device__ __forceinline__ bool aligned16(const void * p) { return (((uintptr_t) p) & 15u) == 0; }
+
+/*
+ * Raw buffer access: a 128-bit resource (base, byte range) in SGPRs, a
+ * per-lane byte offset in one VGPR and a wave-uniform byte offset in an SGPR.
+ * Loads past the range return zero and stores past it are dropped, so ragged
+ * tails need no branches. dword3 = 0x00020000 is the raw 32-bit data format
+ * used by gfx9-family buffer instructions.
+ */
+typedef __attribute__((ext_vector_type(4))) uint32_t u32x4_v;
+#define RAW_BUFFER_DWORD3 0x00020000
+
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void * base, uint32_t num_bytes) {
+	return __builtin_amdgcn_make_buffer_rsrc(const_cast<void *>(base), (short) 0, (int) num_bytes, RAW_BUFFER_DWORD3);
+}
+__device__ __forceinline__ R16 buf_load16(__amdgpu_buffer_rsrc_t r, uint32_t voff, uint32_t soff) {
+	const u32x4_v v = __builtin_amdgcn_raw_buffer_load_b128(r, voff, soff, 0);
+	R16 o;
+	o.w[0] = v.x; o.w[1] = v.y; o.w[2] = v.z; o.w[3] = v.w;
+	return o;
+}
+__device__ __forceinline__ void buf_store16(__amdgpu_buffer_rsrc_t r, uint32_t voff, uint32_t soff, const R16 & x) {
+	const u32x4_v v = {x.w[0], x.w[1], x.w[2], x.w[3]};
+	__builtin_amdgcn_raw_buffer_store_b128(v, r, voff, soff, 0);
+}

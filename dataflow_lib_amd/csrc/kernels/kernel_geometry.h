@@ -1,0 +1,57 @@
+/*
+ * Geometry shared by the kernels and the launch-configuration library (plain
+ * C on the host side), so both sides agree on paths, limits and layouts.
+ *
+ * RMSNorm vector path: each row is split over TPR threads ("a row slot");
+ * thread t of the slot owns the 16-byte chunks t and t + TPR of the row
+ * (RMS_CH = 2 chunks), so it always touches the same columns whatever row it
+ * is on. TPR = 64 * ceil(ceil(chunks_per_row / 2) / 64), at most 1024.
+ * RMSNorm element path (unaligned pointers, ragged rows, or rows longer than
+ * 2 x 1024 chunks): TPR = 256 and a strided loop over the columns.
+ * A workgroup holds `slots` row slots (blockDim.x = slots * TPR).
+ */
+#ifndef KERNEL_GEOMETRY_H
+#define KERNEL_GEOMETRY_H
+
+#define RMS_CH 2
+#define RMS_MAX_TPR 1024
+#define RMS_STREAM_TPR 256
+/* LDS floats per row slot for the row reductions: [2 parities][32] */
+#define RMS_CELLS_PER_SLOT 64
+/* fp32 partial rows for the two-pass dW reduction (16 MiB) */
+#define RMS_DW_SCRATCH_FLOATS (4u << 20)
+
+/* softmax / cross-entropy: one workgroup per row, rows of up to
+ * SMX_THREADS * SMX_MAXCH 16-byte chunks held in registers */
+#define SMX_THREADS 1024
+#define SMX_MAXCH 16
+
+/* RoPE: one wave per token, 4 waves per workgroup, head_dim <= 512 */
+#define ROPE_MAX_HEAD_DIM 512
+#define ROPE_WAVES 4
+
+/* SwiGLU: 16-byte chunks per thread in flight */
+#define SWIGLU_UNROLL 4
+
+#ifdef __HIPCC__
+#define GEOM_FN __host__ __device__ __forceinline__
+#else
+#define GEOM_FN static inline
+#endif
+
+/* RMSNorm: 16-byte chunks per row, or 0 when the element path must be used */
+GEOM_FN int rms_vec_chunks(int n_cols, int elem_bytes, unsigned long long ptr_or) {
+	const int vec = 16 / elem_bytes;
+	if (n_cols <= 0 || (n_cols % vec) != 0 || (ptr_or & 15ull) != 0ull) return 0;
+	const int nv = n_cols / vec;
+	if ((nv + RMS_CH - 1) / RMS_CH > RMS_MAX_TPR) return 0;
+	return nv;
+}
+
+GEOM_FN int rms_tpr_for(int nv) {
+	if (nv == 0) return RMS_STREAM_TPR;
+	const int t = (nv + RMS_CH - 1) / RMS_CH;
+	return ((t + 63) / 64) * 64;
+}
+
+#endif

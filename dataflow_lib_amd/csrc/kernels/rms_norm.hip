@@ -1,0 +1,376 @@
+/*
+ * RMSNorm kernels for gfx950 (hand-written; semantics of the reference's
+ * src/ops/nvidia/norm/rms_norm.cu:4-138,280-412, rms_norm_bwd_x.cu:4-86,175-256,
+ * rms_norm_bwd_w.cu:4-101,211-308, restated in the oracle's rms_norm_*).
+ *
+ * Layout: X, Y, dY, dX row-major [n_rows x n_cols]; W [n_cols];
+ * weighted_sums, rms_vals (= rstd) [n_rows] fp32; dW [n_cols].
+ *
+ * All four ops run on the same row-slot engine (thread layout in
+ * kernel_geometry.h): a slot of TPR threads covers one row with 16-byte accesses,
+ * each thread keeps its W chunks and (bwd_w, fused bwd) its dW partial in
+ * registers for the whole kernel, and row reductions are a DPP wave sum plus
+ * one LDS exchange between the slot's waves.
+ *
+ * dW is reduced in two passes without atomics: each workgroup sums its slots
+ * in slot order through LDS and writes one fp32 partial row to module-scope
+ * scratch; the "_finish" kernel adds the partials in workgroup order.
+ * The result is deterministic. Two dW-reducing ops must not run concurrently
+ * on one device (they share the scratch).
+ */
+#include "dtypes.h"
+#include "reduce.h"
+#include "kernel_geometry.h"
+
+__device__ float g_rms_dw_partials[RMS_DW_SCRATCH_FLOATS];
+/* number of partial rows written by the last main pass (its grid size) */
+__device__ int g_rms_dw_nparts;
+
+enum RmsMode { RMS_FWD = 0, RMS_BWD_X = 1, RMS_BWD_W = 2, RMS_BWD = 3 };
+
+template <typename T> __device__ __forceinline__ float rnd_to(float f) { return to_f(from_f<T>(f)); }
+
+struct RmsArgs {
+	int n_rows, n_cols;
+	float eps;
+	const float * ws_in;      /* bwd_x: fwd weighted sums */
+	const float * rs_in;      /* bwd*: fwd rstd */
+	float * ws_out;           /* fwd outputs (may be NULL) */
+	float * rs_out;
+	const void * W;
+	const void * X;
+	const void * dY;
+	void * Y_or_dX;           /* fwd: Y; bwd_x / bwd: dX (read-modify-write) */
+	void * dW;                /* bwd_w: T; bwd: fp32 */
+};
+
+/* sums of (a, b) over the waves of this thread's slot, one barrier.
+ * cells = LDS [2 parities][slots][32]: a at [w], b at [16 + w]. */
+__device__ __forceinline__ void slot_sum2(float & a, float & b, float * cells, int parity, int slot, int wave_in_slot, int waves_per_slot, int slots) {
+	a = wave_sum(a);
+	b = wave_sum(b);
+	float * c = cells + (parity * slots + slot) * 32;
+	if ((threadIdx.x & 63) == 0) { c[wave_in_slot] = a; c[16 + wave_in_slot] = b; }
+	__syncthreads();
+	float ta = 0.0f, tb = 0.0f;
+	for (int w = 0; w < waves_per_slot; w++) { ta += c[w]; tb += c[16 + w]; }
+	a = ta;
+	b = tb;
+}
+
+/* combine the slots' dW partials (slot order) and write this workgroup's row */
+__device__ __forceinline__ void write_partial_from_lds(const float * colbuf, int n_cols) {
+	__syncthreads();
+	float * part = g_rms_dw_partials + (long) blockIdx.x * n_cols;
+	for (int j = threadIdx.x; j < n_cols; j += blockDim.x) part[j] = colbuf[j];
+}
+
+template <typename T, typename TW, int MODE>
+__device__ __forceinline__ void rms_vector(const RmsArgs & a, int nv, float * lds) {
+	constexpr int V = VecOf<T>::N;
+	const int tpr = rms_tpr_for(nv);
+	const int slots = blockDim.x / tpr;
+	const int slot = threadIdx.x / tpr;
+	const int tr = threadIdx.x % tpr;
+	const int wps = tpr >> 6;
+	const int wis = tr >> 6;
+	const int n_cols = a.n_cols;
+	const R16 * W = reinterpret_cast<const R16 *>(a.W);
+
+	bool own[RMS_CH];
+	R16 wr[RMS_CH];
+	float acc[RMS_CH][V];
+#pragma unroll
+	for (int c = 0; c < RMS_CH; c++) {
+		own[c] = (c * tpr + tr) < nv;
+		if (MODE != RMS_BWD_W) wr[c] = own[c] ? W[c * tpr + tr] : Chunk<T, V>::zero();
+#pragma unroll
+		for (int e = 0; e < V; e++) acc[c][e] = 0.0f;
+	}
+
+	float * cells = lds;                                   /* [2][slots][32] */
+	float * colbuf = lds + RMS_CELLS_PER_SLOT * slots;     /* [n_cols] for the dW modes */
+	int parity = 0;
+
+	for (int base_row = blockIdx.x * slots; base_row < a.n_rows; base_row += gridDim.x * slots) {
+		const int row = base_row + slot;
+		const bool live = row < a.n_rows;
+		const long off = (long) row * (n_cols / V);
+		const R16 * xrow = reinterpret_cast<const R16 *>(a.X) + off;
+		R16 xr[RMS_CH], gr[RMS_CH];
+#pragma unroll
+		for (int c = 0; c < RMS_CH; c++) {
+			const bool ok = live && own[c];
+			xr[c] = ok ? xrow[c * tpr + tr] : Chunk<T, V>::zero();
+			if (MODE != RMS_FWD) gr[c] = ok ? (reinterpret_cast<const R16 *>(a.dY) + off)[c * tpr + tr] : Chunk<T, V>::zero();
+		}
+
+		if (MODE == RMS_FWD) {
+			float ss = 0.0f, sw = 0.0f;
+#pragma unroll
+			for (int c = 0; c < RMS_CH; c++) {
+				float xf[V], wf[V];
+				unpack16<T>(xr[c], xf);
+				unpack16<T>(wr[c], wf);
+#pragma unroll
+				for (int e = 0; e < V; e++) { sw = fmaf(xf[e], wf[e], sw); ss = fmaf(xf[e], xf[e], ss); }
+			}
+			slot_sum2(ss, sw, cells, parity, slot, wis, wps, slots);
+			parity ^= 1;
+			if (live) {
+				const float r = 1.0f / sqrtf(ss / (float) n_cols + a.eps);
+				if (tr == 0) {
+					if (a.ws_out) a.ws_out[row] = sw;
+					if (a.rs_out) a.rs_out[row] = r;
+				}
+				R16 * yrow = reinterpret_cast<R16 *>(a.Y_or_dX) + off;
+#pragma unroll
+				for (int c = 0; c < RMS_CH; c++) {
+					if (own[c]) {
+						float xf[V], wf[V];
+						unpack16<T>(xr[c], xf);
+						unpack16<T>(wr[c], wf);
+#pragma unroll
+						for (int e = 0; e < V; e++) xf[e] = (xf[e] * r) * wf[e];
+						yrow[c * tpr + tr] = pack16<T>(xf);
+					}
+				}
+			}
+		}
+		else if (MODE == RMS_BWD_X) {
+			if (live) {
+				const float r = a.rs_in[row];
+				const float ws = a.ws_in[row];
+				const float r3 = r * r * r;
+				R16 * drow = reinterpret_cast<R16 *>(a.Y_or_dX) + off;
+#pragma unroll
+				for (int c = 0; c < RMS_CH; c++) {
+					if (own[c]) {
+						float wf[V], xf[V], gf[V], df[V];
+						unpack16<T>(wr[c], wf);
+						unpack16<T>(xr[c], xf);
+						unpack16<T>(gr[c], gf);
+						unpack16<T>(drow[c * tpr + tr], df);
+#pragma unroll
+						for (int e = 0; e < V; e++) {
+							const float deriv = wf[e] * r - ((xf[e] * r3) / (float) n_cols) * ws;
+							df[e] = df[e] + rnd_to<T>(gf[e] * rnd_to<T>(deriv));
+						}
+						drow[c * tpr + tr] = pack16<T>(df);
+					}
+				}
+			}
+		}
+		else {
+			const float r = live ? a.rs_in[row] : 0.0f;
+			if (MODE == RMS_BWD) {
+				float dot = 0.0f;
+#pragma unroll
+				for (int c = 0; c < RMS_CH; c++) {
+					float xf[V], gf[V], wf[V];
+					unpack16<T>(xr[c], xf);
+					unpack16<T>(gr[c], gf);
+					unpack16<T>(wr[c], wf);
+#pragma unroll
+					for (int e = 0; e < V; e++) dot = fmaf(gf[e] * wf[e], xf[e], dot);
+				}
+				float unused = 0.0f;
+				slot_sum2(dot, unused, cells, parity, slot, wis, wps, slots);
+				parity ^= 1;
+				if (live) {
+					const float coef = ((r * r * r) * dot) / (float) n_cols;
+					R16 * drow = reinterpret_cast<R16 *>(a.Y_or_dX) + off;
+#pragma unroll
+					for (int c = 0; c < RMS_CH; c++) {
+						if (own[c]) {
+							float xf[V], gf[V], wf[V], df[V];
+							unpack16<T>(xr[c], xf);
+							unpack16<T>(gr[c], gf);
+							unpack16<T>(wr[c], wf);
+							unpack16<T>(drow[c * tpr + tr], df);
+#pragma unroll
+							for (int e = 0; e < V; e++) df[e] = df[e] + (r * (gf[e] * wf[e]) - xf[e] * coef);
+							drow[c * tpr + tr] = pack16<T>(df);
+						}
+					}
+				}
+			}
+			/* dead rows load zeros, so they add nothing */
+#pragma unroll
+			for (int c = 0; c < RMS_CH; c++) {
+				float xf[V], gf[V];
+				unpack16<T>(xr[c], xf);
+				unpack16<T>(gr[c], gf);
+#pragma unroll
+				for (int e = 0; e < V; e++) acc[c][e] = fmaf(gf[e] * xf[e], r, acc[c][e]);
+			}
+		}
+	}
+
+	if (MODE == RMS_BWD_W || MODE == RMS_BWD) {
+		for (int s = 0; s < slots; s++) {
+			__syncthreads();
+			if (slot == s) {
+#pragma unroll
+				for (int c = 0; c < RMS_CH; c++) {
+					if (own[c]) {
+#pragma unroll
+						for (int e = 0; e < V; e++) {
+							const int j = (c * tpr + tr) * V + e;
+							colbuf[j] = (s == 0) ? acc[c][e] : colbuf[j] + acc[c][e];
+						}
+					}
+				}
+			}
+		}
+		write_partial_from_lds(colbuf, n_cols);
+	}
+}
+
+/* element path: any alignment / row length; TPR = 256 */
+template <typename T, typename TW, int MODE>
+__device__ __forceinline__ void rms_stream(const RmsArgs & a, float * lds) {
+	const int tpr = RMS_STREAM_TPR;
+	const int slots = blockDim.x / tpr;
+	const int slot = threadIdx.x / tpr;
+	const int tr = threadIdx.x % tpr;
+	const int wps = tpr >> 6;
+	const int wis = tr >> 6;
+	const int n_cols = a.n_cols;
+	const T * W = reinterpret_cast<const T *>(a.W);
+	float * cells = lds;                                   /* [2][slots][32] */
+	float * colbuf = lds + RMS_CELLS_PER_SLOT * slots;     /* [slots][n_cols] for the dW modes */
+	float * mycol = colbuf + (long) slot * n_cols;
+	if (MODE == RMS_BWD_W || MODE == RMS_BWD) {
+		for (int j = tr; j < n_cols; j += tpr) mycol[j] = 0.0f;
+	}
+	int parity = 0;
+	for (int base_row = blockIdx.x * slots; base_row < a.n_rows; base_row += gridDim.x * slots) {
+		const int row = base_row + slot;
+		const bool live = row < a.n_rows;
+		const long off = (long) row * n_cols;
+		const T * x = reinterpret_cast<const T *>(a.X) + off;
+		const T * g = reinterpret_cast<const T *>(a.dY) + off;
+		T * yd = reinterpret_cast<T *>(a.Y_or_dX) + off;
+		if (MODE == RMS_FWD) {
+			float ss = 0.0f, sw = 0.0f;
+			if (live) {
+				for (int j = tr; j < n_cols; j += tpr) {
+					const float xf = to_f(x[j]);
+					sw = fmaf(xf, to_f(W[j]), sw);
+					ss = fmaf(xf, xf, ss);
+				}
+			}
+			slot_sum2(ss, sw, cells, parity, slot, wis, wps, slots);
+			parity ^= 1;
+			if (live) {
+				const float r = 1.0f / sqrtf(ss / (float) n_cols + a.eps);
+				if (tr == 0) {
+					if (a.ws_out) a.ws_out[row] = sw;
+					if (a.rs_out) a.rs_out[row] = r;
+				}
+				for (int j = tr; j < n_cols; j += tpr) yd[j] = from_f<T>((to_f(x[j]) * r) * to_f(W[j]));
+			}
+		}
+		else if (MODE == RMS_BWD_X) {
+			if (live) {
+				const float r = a.rs_in[row];
+				const float ws = a.ws_in[row];
+				const float r3 = r * r * r;
+				for (int j = tr; j < n_cols; j += tpr) {
+					const float deriv = to_f(W[j]) * r - ((to_f(x[j]) * r3) / (float) n_cols) * ws;
+					yd[j] = from_f<T>(to_f(yd[j]) + rnd_to<T>(to_f(g[j]) * rnd_to<T>(deriv)));
+				}
+			}
+		}
+		else {
+			const float r = live ? a.rs_in[row] : 0.0f;
+			if (MODE == RMS_BWD) {
+				float dot = 0.0f;
+				if (live) {
+					for (int j = tr; j < n_cols; j += tpr) dot = fmaf(to_f(g[j]) * to_f(W[j]), to_f(x[j]), dot);
+				}
+				float unused = 0.0f;
+				slot_sum2(dot, unused, cells, parity, slot, wis, wps, slots);
+				parity ^= 1;
+				if (live) {
+					const float coef = ((r * r * r) * dot) / (float) n_cols;
+					for (int j = tr; j < n_cols; j += tpr) {
+						const float gw = to_f(g[j]) * to_f(W[j]);
+						yd[j] = from_f<T>(to_f(yd[j]) + (r * gw - to_f(x[j]) * coef));
+					}
+				}
+			}
+			if (live) {
+				for (int j = tr; j < n_cols; j += tpr) mycol[j] = fmaf(to_f(g[j]) * to_f(x[j]), r, mycol[j]);
+			}
+		}
+	}
+	if (MODE == RMS_BWD_W || MODE == RMS_BWD) {
+		__syncthreads();
+		/* slot order: slot 0 accumulates the others */
+		if (slot == 0) {
+			for (int s = 1; s < slots; s++)
+				for (int j = tr; j < n_cols; j += tpr) mycol[j] += colbuf[(long) s * n_cols + j];
+		}
+		write_partial_from_lds(colbuf, n_cols);
+	}
+}
+
+template <typename T, typename TW, int MODE>
+__device__ __forceinline__ void rms_run(const RmsArgs & a) {
+	extern __shared__ float lds[];
+	if ((MODE == RMS_BWD_W || MODE == RMS_BWD) && blockIdx.x == 0 && threadIdx.x == 0) g_rms_dw_nparts = (int) gridDim.x;
+	unsigned long long ptr_or = (unsigned long long) (uintptr_t) a.X;
+	if (MODE != RMS_BWD_W) ptr_or |= (unsigned long long) (uintptr_t) a.W;
+	if (MODE != RMS_FWD) ptr_or |= (unsigned long long) (uintptr_t) a.dY;
+	if (MODE != RMS_BWD_W) ptr_or |= (unsigned long long) (uintptr_t) a.Y_or_dX;
+	const int nv = rms_vec_chunks(a.n_cols, (int) sizeof(T), ptr_or);
+	if (nv > 0) rms_vector<T, TW, MODE>(a, nv, lds);
+	else rms_stream<T, TW, MODE>(a, lds);
+}
+
+/* finish: dW[j] = rnd(dW[j] + sum_g partial[g][j]), partials in workgroup order */
+template <typename TW>
+__device__ __forceinline__ void rms_dw_finish(int n_cols, TW * dW) {
+	const int j = blockIdx.x * blockDim.x + threadIdx.x;
+	if (j >= n_cols) return;
+	const int n_parts = g_rms_dw_nparts;
+	float s = 0.0f;
+	for (int g = 0; g < n_parts; g++) s += g_rms_dw_partials[(long) g * n_cols + j];
+	dW[j] = from_f<TW>(to_f(dW[j]) + s);
+}
+
+#define RMS_KERNELS(FSUF, PSUF, T)                                                                                       \
+	extern "C" __global__ void __launch_bounds__(1024) rms_norm_##FSUF##_kernel(int n_rows, int n_cols, float eps,       \
+			T * rms_weight, T * X, T * out, float * weighted_sums, float * rms_vals) {                                  \
+		RmsArgs a = {n_rows, n_cols, eps, nullptr, nullptr, weighted_sums, rms_vals, rms_weight, X, nullptr, out, nullptr}; \
+		rms_run<T, T, RMS_FWD>(a);                                                                                       \
+	}                                                                                                                    \
+	extern "C" __global__ void __launch_bounds__(1024) rms_norm_bwd_x_##PSUF##_kernel(int n_rows, int n_cols, float eps, \
+			float * fwd_weighted_sums, float * fwd_rms_vals, T * rms_weight, T * X_inp, T * upstream_dX, T * dX) {       \
+		RmsArgs a = {n_rows, n_cols, eps, fwd_weighted_sums, fwd_rms_vals, nullptr, nullptr, rms_weight, X_inp, upstream_dX, dX, nullptr}; \
+		rms_run<T, T, RMS_BWD_X>(a);                                                                                     \
+	}                                                                                                                    \
+	extern "C" __global__ void __launch_bounds__(1024) rms_norm_bwd_w_##PSUF##_kernel(int n_rows, int n_cols, float eps, \
+			float * fwd_rms_vals, T * X_inp, T * upstream_dX, T * dW) {                                                 \
+		RmsArgs a = {n_rows, n_cols, eps, nullptr, fwd_rms_vals, nullptr, nullptr, nullptr, X_inp, upstream_dX, nullptr, dW}; \
+		rms_run<T, T, RMS_BWD_W>(a);                                                                                     \
+	}                                                                                                                    \
+	extern "C" __global__ void __launch_bounds__(256) rms_norm_bwd_w_##PSUF##_kernel_finish(int n_rows, int n_cols,      \
+			float eps, float * fwd_rms_vals, T * X_inp, T * upstream_dX, T * dW) {                                      \
+		rms_dw_finish<T>(n_cols, dW);                                                                                    \
+	}                                                                                                                    \
+	extern "C" __global__ void __launch_bounds__(1024) rms_norm_bwd_##PSUF##_kernel(int n_rows, int n_cols, float eps,   \
+			float * fwd_rms_vals, T * rms_weight, T * X_inp, T * upstream_dX, T * dX, float * dW) {                     \
+		RmsArgs a = {n_rows, n_cols, eps, nullptr, fwd_rms_vals, nullptr, nullptr, rms_weight, X_inp, upstream_dX, dX, dW}; \
+		rms_run<T, float, RMS_BWD>(a);                                                                                   \
+	}                                                                                                                    \
+	extern "C" __global__ void __launch_bounds__(256) rms_norm_bwd_##PSUF##_kernel_finish(int n_rows, int n_cols,        \
+			float eps, float * fwd_rms_vals, T * rms_weight, T * X_inp, T * upstream_dX, T * dX, float * dW) {          \
+		rms_dw_finish<float>(n_cols, dW);                                                                                \
+	}
+
+RMS_KERNELS(fp32, fp32_fp32, float)
+RMS_KERNELS(fp16, fp16_fp16, f16_t)
+RMS_KERNELS(bf16, bf16_bf16, bf16_t)

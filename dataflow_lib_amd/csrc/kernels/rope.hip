@@ -1,0 +1,150 @@
+/*
+ * Rotary position embedding, forward and backward, in place on Q and K
+ * (semantics of the reference's src/ops/nvidia/attention/rope.cu:3-57,123-180
+ * and rope_bwd_x.cu:3-60,120-175; restated in the oracle's rope_* functions).
+ *
+ * Q is [T x model_dim], K is [T x num_kv_heads*head_dim], T = N / model_dim,
+ * row-major, heads contiguous inside a row. Pairs are adjacent elements
+ * (2p, 2p+1) of a head; pair p of token t turns by
+ *   arg = (float) pos[t] * angle_p,   angle_p = (float) theta^(-(2p)/head_dim)
+ * with angle_p and the fp32 product formed exactly as the reference does.
+ *
+ * One wave64 per token. angle_p is computed once per wave (fp64 pow, rounded
+ * to fp32). Per token each lane evaluates cos/sin of one pair argument in
+ * fp64 (rounded to fp32) into a per-wave LDS table shared by all 40 heads of
+ * the token; the rotation uses a compensated fp32 two-term dot product, so
+ * the fp32 result is within ~1 ulp even when the two products cancel.
+ */
+#include "dtypes.h"
+#include "kernel_geometry.h"
+
+/* a*b + c*d, with the rounding error of c*d added back */
+__device__ __forceinline__ float dot2c(float a, float b, float c, float d) {
+	const float p = c * d;
+	const float pe = fmaf(c, d, -p);
+	return fmaf(a, b, p) + pe;
+}
+
+template <bool BWD>
+__device__ __forceinline__ void rotate(float c, float s, float e, float o, float & e2, float & o2) {
+	if (!BWD) {
+		e2 = dot2c(c, e, -s, o);   /* c*e - s*o */
+		o2 = dot2c(c, o, s, e);    /* c*o + s*e */
+	}
+	else {
+		e2 = dot2c(c, e, s, o);    /* c*e + s*o */
+		o2 = dot2c(c, o, -s, e);   /* c*o - s*e */
+	}
+}
+
+__device__ __forceinline__ void wave_lds_sync() {
+	__builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
+	__builtin_amdgcn_wave_barrier();
+	__builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup");
+}
+
+/* rotate one row (Q or K) of `width` elements with the token's table */
+template <typename T, bool BWD, bool VECTOR>
+__device__ __forceinline__ void rope_row(T * row, int width, int head_dim, const float2 * cs, int lane) {
+	if (VECTOR) {
+		constexpr int VEC = VecOf<T>::N;
+		const int nv = width / VEC;
+		const int step = (64 * VEC) % head_dim;
+		int col = (lane * VEC) % head_dim;
+		R16 * rv = reinterpret_cast<R16 *>(row);
+		for (int v = lane; v < nv; v += 64) {
+			float f[VEC];
+			unpack16<T>(rv[v], f);
+			const int p0 = col >> 1;
+#pragma unroll
+			for (int q = 0; q < VEC / 2; q++) {
+				const float2 t = cs[p0 + q];
+				rotate<BWD>(t.x, t.y, f[2 * q], f[2 * q + 1], f[2 * q], f[2 * q + 1]);
+			}
+			rv[v] = pack16<T>(f);
+			col += step;
+			if (col >= head_dim) col -= head_dim;
+		}
+	}
+	else {
+		const int npairs = width >> 1;
+		const int step = 128 % head_dim;
+		int col = (lane * 2) % head_dim;
+		for (int p = lane; p < npairs; p += 64) {
+			const float2 t = cs[col >> 1];
+			float e2, o2;
+			rotate<BWD>(t.x, t.y, to_f(row[2 * p]), to_f(row[2 * p + 1]), e2, o2);
+			row[2 * p] = from_f<T>(e2);
+			row[2 * p + 1] = from_f<T>(o2);
+			col += step;
+			if (col >= head_dim) col -= head_dim;
+		}
+	}
+}
+
+template <typename T, bool BWD>
+__device__ __forceinline__ void rope_impl(uint64_t N, int model_dim, int head_dim, int num_kv_heads, int theta,
+											const int * seq_positions, T * X_q, T * X_k) {
+	__shared__ float2 tables[ROPE_WAVES][ROPE_MAX_HEAD_DIM / 2];
+	const int lane = threadIdx.x & 63;
+	const int wave = threadIdx.x >> 6;
+	const int wpb = blockDim.x >> 6;
+	const long n_tokens = (long) (N / (uint64_t) model_dim);
+	const int kv_dim = num_kv_heads * head_dim;
+	const int half = head_dim >> 1;
+	float2 * cs = tables[wave];
+
+	/* angle_p for p = lane + 64k, exactly as the reference's fp32 expression
+	 * powf(theta, -((float) c / (float) head_dim)) evaluated correctly rounded */
+	float ang[ROPE_MAX_HEAD_DIM / 128];
+#pragma unroll
+	for (int k = 0; k < ROPE_MAX_HEAD_DIM / 128; k++) {
+		const int p = lane + 64 * k;
+		ang[k] = 0.0f;
+		if (p < half) {
+			const float expo = -((float) (2 * p) / (float) head_dim);
+			ang[k] = (float) pow((double) (float) theta, (double) expo);
+		}
+	}
+
+	constexpr int VEC = VecOf<T>::N;
+	const bool vec_ok = (head_dim % VEC == 0) && aligned16(X_q) && aligned16(X_k);
+
+	for (long t = (long) blockIdx.x * wpb + wave; t < n_tokens; t += (long) gridDim.x * wpb) {
+		const float fpos = (float) seq_positions[t];
+#pragma unroll
+		for (int k = 0; k < ROPE_MAX_HEAD_DIM / 128; k++) {
+			const int p = lane + 64 * k;
+			if (p < half) {
+				const float arg = fpos * ang[k];
+				double sd, cd;
+				sincos((double) arg, &sd, &cd);
+				cs[p] = make_float2((float) cd, (float) sd);
+			}
+		}
+		wave_lds_sync();
+		if (vec_ok) {
+			rope_row<T, BWD, true>(X_q + t * model_dim, model_dim, head_dim, cs, lane);
+			rope_row<T, BWD, true>(X_k + t * kv_dim, kv_dim, head_dim, cs, lane);
+		}
+		else {
+			rope_row<T, BWD, false>(X_q + t * model_dim, model_dim, head_dim, cs, lane);
+			rope_row<T, BWD, false>(X_k + t * kv_dim, kv_dim, head_dim, cs, lane);
+		}
+		wave_lds_sync();
+	}
+}
+
+#define ROPE_KERNELS(SUFFIX, T)                                                                                     \
+	extern "C" __global__ void __launch_bounds__(256) rope_##SUFFIX##_kernel(uint64_t N, int model_dim, int head_dim, \
+			int num_kv_heads, int theta, int * seq_positions, T * X_q, T * X_k) {                                    \
+		rope_impl<T, false>(N, model_dim, head_dim, num_kv_heads, theta, seq_positions, X_q, X_k);                  \
+	}                                                                                                               \
+	extern "C" __global__ void __launch_bounds__(256) rope_bwd_x_##SUFFIX##_kernel(uint64_t N, int model_dim, int head_dim, \
+			int num_kv_heads, int theta, int * seq_positions, T * dX_q, T * dX_k) {                                  \
+		rope_impl<T, true>(N, model_dim, head_dim, num_kv_heads, theta, seq_positions, dX_q, dX_k);                 \
+	}
+
+ROPE_KERNELS(fp32, float)
+ROPE_KERNELS(fp16, f16_t)
+ROPE_KERNELS(bf16, bf16_t)

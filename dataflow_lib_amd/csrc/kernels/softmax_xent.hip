@@ -1,0 +1,263 @@
+/*
+ * Softmax, cross-entropy and the fused softmax + cross-entropy
+ * (semantics of the reference's src/ops/nvidia/loss/softmax.cu:3-140,273-407
+ * and the intended semantics of cross_entropy.cu:4-44; restated in the
+ * oracle's softmax / cross_entropy_loss / softmax_cross_entropy_loss).
+ *
+ * Per row, exactly as the reference orders the arithmetic:
+ *   m   = max_j x_j                          (exact)
+ *   d_j = rnd(x_j - m)                       (rounded to the input type; fp32: plain fp32 difference)
+ *   s   = sum_j exp(d_j)
+ *   y_j = rnd_out(exp(d_j) / s)
+ * cross-entropy subtracts 1 at the label in the output type:
+ *   y_l = rnd_out(y_l - 1)
+ * and the fused op also writes loss_r = log(sum_j exp(x_j - m)) + m - x_l
+ * (from the unrounded differences) and mean_loss = sum_r loss_r / n_rows.
+ *
+ * gfx950 design: one 1024-thread workgroup per row; the whole row
+ * (up to 16 x 16 B per thread = 128K bf16 logits) is held in VGPRs, so each
+ * element is read from HBM once and written once. After the max pass the
+ * registers are overwritten with d_j (exact in the storage type), so the
+ * output pass needs no recomputation of x - m. exp uses the hardware exp2.
+ * mean_loss is finished by the last workgroup to arrive (atomic ticket),
+ * summing loss[] in row order, so it is deterministic.
+ */
+#include "dtypes.h"
+#include "reduce.h"
+#include "kernel_geometry.h"
+
+#define SMX_LOG2E 1.4426950408889634f
+
+/* arrival ticket for the mean-loss finish; reset by the last workgroup */
+__device__ unsigned int g_xent_arrivals;
+
+__device__ __forceinline__ float exp_fast(float x) { return __builtin_amdgcn_exp2f(x * SMX_LOG2E); }
+
+template <typename T> __device__ __forceinline__ float rnd_in(float f) { return to_f(from_f<T>(f)); }
+
+/* Block reduction of up to two values; slots = LDS [2][16]. Ends with a
+ * barrier-protected read, and the caller separates consecutive uses with
+ * another barrier. */
+__device__ __forceinline__ float block_max(float v, float * slots) {
+	v = wave_max(v);
+	const int nw = blockDim.x >> 6;
+	if ((threadIdx.x & 63) == 0) slots[threadIdx.x >> 6] = v;
+	__syncthreads();
+	float m = slots[0];
+	for (int w = 1; w < nw; w++) m = fmaxf(m, slots[w]);
+	return m;
+}
+
+__device__ __forceinline__ void block_sum2(float & a, float & b, float * slots) {
+	a = wave_sum(a);
+	b = wave_sum(b);
+	const int nw = blockDim.x >> 6;
+	if ((threadIdx.x & 63) == 0) { slots[threadIdx.x >> 6] = a; slots[16 + (threadIdx.x >> 6)] = b; }
+	__syncthreads();
+	float sa = 0.0f, sb = 0.0f;
+	for (int w = 0; w < nw; w++) { sa += slots[w]; sb += slots[16 + w]; }
+	a = sa;
+	b = sb;
+}
+
+/* last workgroup to arrive sums loss[] in row order */
+__device__ __forceinline__ void finish_mean_loss(int n_rows, const float * loss, float * mean_loss, double * dslots) {
+	__shared__ int is_last;
+	__syncthreads();
+	if (threadIdx.x == 0) {
+		__threadfence();
+		const unsigned int prev = __hip_atomic_fetch_add(&g_xent_arrivals, 1u, __ATOMIC_ACQ_REL, __HIP_MEMORY_SCOPE_AGENT);
+		is_last = (prev == gridDim.x - 1) ? 1 : 0;
+	}
+	__syncthreads();
+	if (!is_last) return;
+	__threadfence();
+	double s = 0.0;
+	for (int r = threadIdx.x; r < n_rows; r += blockDim.x) s += (double) loss[r];
+	/* fixed-order tree over the 16 waves via LDS */
+	for (int off = 32; off > 0; off >>= 1) s += __shfl_xor(s, off);
+	if ((threadIdx.x & 63) == 0) dslots[threadIdx.x >> 6] = s;
+	__syncthreads();
+	if (threadIdx.x == 0) {
+		double t = 0.0;
+		for (int w = 0; w < (int) (blockDim.x >> 6); w++) t += dslots[w];
+		*mean_loss = (float) (t / (double) n_rows);
+		g_xent_arrivals = 0u;
+	}
+}
+
+/* register-resident row path: rows of at most SMX_MAXCH 16-byte chunks per
+ * thread; chunk c of thread t is row chunk c * blockDim.x + t, addressed
+ * through a per-row buffer resource (one VGPR offset for all chunks) */
+template <typename T, typename TO, bool FUSED>
+__device__ __forceinline__ void smx_regs(int n_rows, int n_cols, const T * X, TO * out, const uint32_t * labels, float * loss) {
+	constexpr int VEC = VecOf<T>::N;
+	static_assert(sizeof(T) == sizeof(TO), "in-register output packing needs equal widths");
+	__shared__ float slots[32];
+	const int tid = threadIdx.x;
+	const int nt = blockDim.x;
+	const int nv = n_cols / VEC;
+	const int nch = (nv + nt - 1) / nt;
+	const uint32_t row_bytes = (uint32_t) n_cols * (uint32_t) sizeof(T);
+	const uint32_t voff = (uint32_t) tid * 16u;
+	const uint32_t cstride = (uint32_t) nt * 16u;
+
+	for (int row = blockIdx.x; row < n_rows; row += gridDim.x) {
+		const __amdgpu_buffer_rsrc_t rin = make_rsrc(X + (long) row * n_cols, row_bytes);
+		const __amdgpu_buffer_rsrc_t rout = make_rsrc(out + (long) row * n_cols, row_bytes);
+		uint32_t lab = 0xffffffffu;
+		float x_lab = 0.0f;
+		if (FUSED) {
+			lab = labels[row];
+			if (tid == 0 && lab < (uint32_t) n_cols) x_lab = to_f(X[(long) row * n_cols + lab]);
+		}
+
+		R16 xr[SMX_MAXCH];
+		/* max pass; the fused op also accumulates sx = sum exp(x - m_run)
+		 * against a running max, rescaled once per chunk */
+		float m = -__builtin_inff();
+		float sx = 0.0f;
+#pragma unroll
+		for (int c = 0; c < SMX_MAXCH; c++) {
+			if (c < nch) {
+				xr[c] = buf_load16(rin, voff, c * cstride);
+				float f[VEC];
+				unpack16<T>(xr[c], f);
+				float cm = f[0];
+#pragma unroll
+				for (int e = 1; e < VEC; e++) cm = fmaxf(cm, f[e]);
+				/* chunks past the row end hold zeros: keep them out of the max */
+				if (c * nt + tid >= nv) cm = -__builtin_inff();
+				if (FUSED) {
+					const float mn = fmaxf(m, cm);
+					if (cm != -__builtin_inff()) {
+						if (mn != m) sx *= exp_fast(m - mn);
+#pragma unroll
+						for (int e = 0; e < VEC; e++) sx += exp_fast(f[e] - mn);
+					}
+					m = mn;
+				}
+				else {
+					m = fmaxf(m, cm);
+				}
+			}
+		}
+		const float m_thread = m;
+		m = block_max(m, slots);
+		if (FUSED) sx = (m_thread == -__builtin_inff()) ? 0.0f : sx * exp_fast(m_thread - m);
+
+		float sd = 0.0f;
+#pragma unroll
+		for (int c = 0; c < SMX_MAXCH; c++) {
+			if (c < nch && c * nt + tid < nv) {
+				float f[VEC];
+				unpack16<T>(xr[c], f);
+#pragma unroll
+				for (int e = 0; e < VEC; e++) {
+					f[e] = rnd_in<T>(f[e] - m);
+					sd += exp_fast(f[e]);
+				}
+				xr[c] = pack16<T>(f);   /* d is exact in T */
+			}
+		}
+		__syncthreads();   /* slots reuse */
+		block_sum2(sd, sx, slots);
+		const float inv = 1.0f / sd;
+
+		/* chunk and lane holding the label (if any) */
+		const int lab_chunk = (lab < (uint32_t) n_cols) ? (int) (lab / VEC) : -1;
+#pragma unroll
+		for (int c = 0; c < SMX_MAXCH; c++) {
+			if (c < nch) {
+				float f[VEC];
+				unpack16<T>(xr[c], f);
+#pragma unroll
+				for (int e = 0; e < VEC; e++) f[e] = exp_fast(f[e]) * inv;
+				if (FUSED && (c * nt + tid) == lab_chunk) {
+					const int le = (int) (lab % VEC);
+#pragma unroll
+					for (int e = 0; e < VEC; e++)
+						if (e == le) f[e] = rnd_in<TO>(f[e]) - 1.0f;
+				}
+				buf_store16(rout, voff, c * cstride, pack16<TO>(f));
+			}
+		}
+		if (FUSED && tid == 0 && loss) {
+			loss[row] = (lab < (uint32_t) n_cols) ? (logf(sx) + m - x_lab) : __builtin_nanf("");
+		}
+		__syncthreads();   /* slots reuse by the next row */
+	}
+}
+
+/* any row length / alignment: three passes over global memory per row */
+template <typename T, typename TO, bool FUSED>
+__device__ __forceinline__ void smx_stream(int n_rows, int n_cols, const T * X, TO * out, const uint32_t * labels, float * loss) {
+	__shared__ float slots[32];
+	const int tid = threadIdx.x;
+	const int nt = blockDim.x;
+	for (int row = blockIdx.x; row < n_rows; row += gridDim.x) {
+		const T * xrow = X + (long) row * n_cols;
+		TO * orow = out + (long) row * n_cols;
+		uint32_t lab = 0xffffffffu;
+		float x_lab = 0.0f;
+		if (FUSED) {
+			lab = labels[row];
+			if (tid == 0 && lab < (uint32_t) n_cols) x_lab = to_f(xrow[lab]);
+		}
+		float m = -__builtin_inff();
+		for (int j = tid; j < n_cols; j += nt) m = fmaxf(m, to_f(xrow[j]));
+		m = block_max(m, slots);
+		float sd = 0.0f, sx = 0.0f;
+		for (int j = tid; j < n_cols; j += nt) {
+			const float diff = to_f(xrow[j]) - m;
+			sd += exp_fast(rnd_in<T>(diff));
+			if (FUSED) sx += exp_fast(diff);
+		}
+		__syncthreads();
+		block_sum2(sd, sx, slots);
+		const float inv = 1.0f / sd;
+		for (int j = tid; j < n_cols; j += nt) {
+			float y = exp_fast(rnd_in<T>(to_f(xrow[j]) - m)) * inv;
+			if (FUSED && (uint32_t) j == lab) y = rnd_in<TO>(y) - 1.0f;
+			orow[j] = from_f<TO>(y);
+		}
+		if (FUSED && tid == 0 && loss) {
+			loss[row] = (lab < (uint32_t) n_cols) ? (logf(sx) + m - x_lab) : __builtin_nanf("");
+		}
+		__syncthreads();
+	}
+}
+
+template <typename T, typename TO, bool FUSED>
+__device__ __forceinline__ void smx(int n_rows, int n_cols, const T * X, TO * out, const uint32_t * labels, float * loss, float * mean_loss) {
+	constexpr int VEC = VecOf<T>::N;
+	__shared__ double dslots[16];
+	const bool vec_ok = (n_cols % VEC == 0) && aligned16(X) && aligned16(out)
+						&& ((n_cols / VEC + (int) blockDim.x - 1) / (int) blockDim.x) <= SMX_MAXCH;
+	if (vec_ok) smx_regs<T, TO, FUSED>(n_rows, n_cols, X, out, labels, loss);
+	else smx_stream<T, TO, FUSED>(n_rows, n_cols, X, out, labels, loss);
+	if (FUSED && mean_loss && loss) finish_mean_loss(n_rows, loss, mean_loss, dslots);
+}
+
+#define SMX_KERNELS(SUFFIX, PSUFFIX, T)                                                                                \
+	extern "C" __global__ void __launch_bounds__(SMX_THREADS) softmax_##PSUFFIX##_kernel(int n_rows, int n_cols,       \
+			T * X, T * out) {                                                                                          \
+		smx<T, T, false>(n_rows, n_cols, X, out, nullptr, nullptr, nullptr);                                           \
+	}                                                                                                                  \
+	extern "C" __global__ void __launch_bounds__(SMX_THREADS) softmax_cross_entropy_loss_##SUFFIX##_kernel(int n_rows, \
+			int n_cols, T * logits, uint32_t * labels, float * loss, float * mean_loss) {                              \
+		smx<T, T, true>(n_rows, n_cols, logits, logits, labels, loss, mean_loss);                                      \
+	}                                                                                                                  \
+	extern "C" __global__ void __launch_bounds__(256) cross_entropy_loss_##SUFFIX##_kernel(int n_rows, int n_cols,     \
+			T * pred_logits, uint32_t * labels) {                                                                      \
+		const long r = (long) blockIdx.x * blockDim.x + threadIdx.x;                                                   \
+		if (r >= n_rows) return;                                                                                       \
+		const uint32_t lab = labels[r];                                                                                \
+		if (lab >= (uint32_t) n_cols) return;                                                                          \
+		T * p = pred_logits + r * (long) n_cols + lab;                                                                 \
+		*p = from_f<T>(to_f(*p) - 1.0f);                                                                               \
+	}
+
+SMX_KERNELS(fp32, fp32_fp32, float)
+SMX_KERNELS(fp16, fp16_fp16, f16_t)
+SMX_KERNELS(bf16, bf16_bf16, bf16_t)

@@ -1,0 +1,125 @@
+/*
+ * SwiGLU forward and backward (semantics of the reference's
+ * src/ops/nvidia/activations/swiglu.cu:4-68 and swiglu_bwd_x.cu:4-80;
+ * restated in the oracle's swiglu_* functions).
+ *
+ *   fwd: out = silu(g) * u,  silu(g) = g * sigmoid(g)
+ *   bwd: dU = dO * silu(g);  dG = dO * u * s * (1 + g * (1 - s)),  s = sigmoid(g)
+ *
+ * The backward uses the sigmoid form of the reference's closed form
+ * u*(1+e+g*e)/(1+e)^2 (e = exp(-g)); it is the same function, and it stays
+ * finite where the reference's form gives inf - inf = NaN (g < -88.7).
+ *
+ * Pure streaming: the [rows x cols] tensors are treated as flat arrays,
+ * grid-stride over 16-byte chunks, four chunks per thread in flight.
+ */
+#include "dtypes.h"
+#include "kernel_geometry.h"
+
+#define LOG2E_F 1.4426950408889634f
+
+/* 1 / (1 + exp(-g)) with the hardware exp2 and reciprocal */
+__device__ __forceinline__ float sigmoidf_fast(float g) {
+	return __builtin_amdgcn_rcpf(1.0f + __builtin_amdgcn_exp2f(-g * LOG2E_F));
+}
+
+template <typename T>
+__device__ __forceinline__ void swiglu_fwd(long n, const T * g, const T * u, T * out) {
+	constexpr int VEC = VecOf<T>::N;
+	const long nth = (long) gridDim.x * blockDim.x;
+	const long tid = (long) blockIdx.x * blockDim.x + threadIdx.x;
+	const bool vec_ok = aligned16(g) && aligned16(u) && aligned16(out);
+	const long nvec = vec_ok ? n / VEC : 0;
+	const R16 * gv = reinterpret_cast<const R16 *>(g);
+	const R16 * uv = reinterpret_cast<const R16 *>(u);
+	R16 * ov = reinterpret_cast<R16 *>(out);
+
+	for (long v0 = tid; v0 < nvec; v0 += nth * SWIGLU_UNROLL) {
+		R16 gr[SWIGLU_UNROLL], ur[SWIGLU_UNROLL];
+#pragma unroll
+		for (int k = 0; k < SWIGLU_UNROLL; k++) {
+			const long v = v0 + k * nth;
+			if (v < nvec) { gr[k] = gv[v]; ur[k] = uv[v]; }
+		}
+#pragma unroll
+		for (int k = 0; k < SWIGLU_UNROLL; k++) {
+			const long v = v0 + k * nth;
+			if (v < nvec) {
+				float gf[VEC], uf[VEC], of[VEC];
+				unpack16<T>(gr[k], gf);
+				unpack16<T>(ur[k], uf);
+#pragma unroll
+				for (int e = 0; e < VEC; e++) of[e] = (gf[e] * sigmoidf_fast(gf[e])) * uf[e];
+				ov[v] = pack16<T>(of);
+			}
+		}
+	}
+	for (long i = nvec * VEC + tid; i < n; i += nth) {
+		const float gf = to_f(g[i]);
+		out[i] = from_f<T>((gf * sigmoidf_fast(gf)) * to_f(u[i]));
+	}
+}
+
+template <typename T>
+__device__ __forceinline__ void swiglu_bwd_elem(float g, float u, float d, float & dg, float & du) {
+	const float s = sigmoidf_fast(g);
+	du = d * (g * s);
+	dg = d * (u * s * fmaf(g, 1.0f - s, 1.0f));
+}
+
+template <typename T>
+__device__ __forceinline__ void swiglu_bwd(long n, const T * g, const T * u, const T * dO, T * dG, T * dU) {
+	constexpr int VEC = VecOf<T>::N;
+	const long nth = (long) gridDim.x * blockDim.x;
+	const long tid = (long) blockIdx.x * blockDim.x + threadIdx.x;
+	const bool vec_ok = aligned16(g) && aligned16(u) && aligned16(dO) && aligned16(dG) && aligned16(dU);
+	const long nvec = vec_ok ? n / VEC : 0;
+	const R16 * gv = reinterpret_cast<const R16 *>(g);
+	const R16 * uv = reinterpret_cast<const R16 *>(u);
+	const R16 * dv = reinterpret_cast<const R16 *>(dO);
+	R16 * dgv = reinterpret_cast<R16 *>(dG);
+	R16 * duv = reinterpret_cast<R16 *>(dU);
+
+	for (long v0 = tid; v0 < nvec; v0 += nth * SWIGLU_UNROLL) {
+		R16 gr[SWIGLU_UNROLL], ur[SWIGLU_UNROLL], dr[SWIGLU_UNROLL];
+#pragma unroll
+		for (int k = 0; k < SWIGLU_UNROLL; k++) {
+			const long v = v0 + k * nth;
+			if (v < nvec) { gr[k] = gv[v]; ur[k] = uv[v]; dr[k] = dv[v]; }
+		}
+#pragma unroll
+		for (int k = 0; k < SWIGLU_UNROLL; k++) {
+			const long v = v0 + k * nth;
+			if (v < nvec) {
+				float gf[VEC], uf[VEC], df[VEC], ogf[VEC], ouf[VEC];
+				unpack16<T>(gr[k], gf);
+				unpack16<T>(ur[k], uf);
+				unpack16<T>(dr[k], df);
+#pragma unroll
+				for (int e = 0; e < VEC; e++) swiglu_bwd_elem<T>(gf[e], uf[e], df[e], ogf[e], ouf[e]);
+				dgv[v] = pack16<T>(ogf);
+				duv[v] = pack16<T>(ouf);
+			}
+		}
+	}
+	for (long i = nvec * VEC + tid; i < n; i += nth) {
+		float dg, du;
+		swiglu_bwd_elem<T>(to_f(g[i]), to_f(u[i]), to_f(dO[i]), dg, du);
+		dG[i] = from_f<T>(dg);
+		dU[i] = from_f<T>(du);
+	}
+}
+
+#define SWIGLU_KERNELS(SUFFIX, BSUFFIX, T)                                                                           \
+	extern "C" __global__ void __launch_bounds__(256) swiglu_##SUFFIX##_kernel(int num_rows, int num_cols,          \
+			T * x_w1, T * x_w3, T * out) {                                                                           \
+		swiglu_fwd<T>((long) num_rows * (long) num_cols, x_w1, x_w3, out);                                           \
+	}                                                                                                                \
+	extern "C" __global__ void __launch_bounds__(256) swiglu_bwd_x_##BSUFFIX##_kernel(int num_rows, int num_cols,  \
+			T * x_w1, T * x_w3, T * upstream_dX, T * dX_w1, T * dX_w3) {                                             \
+		swiglu_bwd<T>((long) num_rows * (long) num_cols, x_w1, x_w3, upstream_dX, dX_w1, dX_w3);                    \
+	}
+
+SWIGLU_KERNELS(fp32, fp32_fp32, float)
+SWIGLU_KERNELS(fp16, fp16_fp16, f16_t)
+SWIGLU_KERNELS(bf16, bf16_bf16, bf16_t)

@@ -1,0 +1,106 @@
+/*
+ * Op API: each submit_* fills an Op (skeleton + pointers to its arguments)
+ * and hands it to handle->submit_op. Returns 0, or -1 with a message on
+ * stderr. Argument order and meaning follow the reference's
+ * src/dataflow_ops/include/dataflow_ops.h:146-215. The external-library ops
+ * of the reference (matmul, attention) are not part of this library.
+ */
+#ifndef DATAFLOW_OPS_H
+#define DATAFLOW_OPS_H
+
+#include "dataflow.h"
+#include "ops.h"
+#include "dataflow_handle.h"
+#include "set_native_op_skeletons.h"
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* --- norm (reference: src/dataflow_ops/src/norm_ops.c:4-97) --- */
+
+/* out = (X * rstd) * w per row; weighted_sums[r] = sum_j X*w, rms_vals[r] = rstd
+ * = 1/sqrt(mean(X^2) + eps); each of the two may be NULL. */
+int submit_rms_norm(Dataflow_Handle * handle, int stream_id,
+						DataflowDatatype fwd_dt,
+						int n_rows, int n_cols, float eps,
+						void * rms_weight, void * X, void * out, float * weighted_sums, float * rms_vals);
+
+/* dX += dY * bf(w*r - (x*r^3/n)*ws) with the reference's intermediate
+ * roundings to bwd_dt (not the exact gradient; see submit_rms_norm_bwd). */
+int submit_rms_norm_bwd_x(Dataflow_Handle * handle, int stream_id,
+								DataflowDatatype fwd_dt, DataflowDatatype bwd_dt,
+								int n_rows, int n_cols, float eps,
+								float * fwd_weighted_sums, float * fwd_rms_vals,
+								void * rms_weight, void * X_inp, void * upstream_dX, void * dX);
+
+/* dW += sum over rows of dY * X * rstd (deterministic order). */
+int submit_rms_norm_bwd_w(Dataflow_Handle * handle, int stream_id,
+								DataflowDatatype fwd_dt, DataflowDatatype bwd_dt,
+								int n_rows, int n_cols, float eps,
+								float * fwd_rms_vals, void * X_inp, void * upstream_dX, void * dW);
+
+/* Fused exact-gradient backward: dX += exact dL/dX, dW (fp32) += dL/dW, one
+ * pass over X and dY. No reference counterpart. */
+int submit_rms_norm_bwd(Dataflow_Handle * handle, int stream_id,
+								DataflowDatatype fwd_dt, DataflowDatatype bwd_dt,
+								int n_rows, int n_cols, float eps,
+								float * fwd_rms_vals, void * rms_weight, void * X_inp, void * upstream_dX, void * dX, float * dW);
+
+/* --- attention misc (reference: src/dataflow_ops/src/attn_misc_ops.c:3-65) --- */
+
+/* In-place rotary embedding of adjacent (even, odd) pairs of X_q
+ * [N / model_dim tokens x model_dim] and X_k [tokens x num_kv_heads*head_dim];
+ * angle = pos * theta^(-c/head_dim) for pair column c. */
+int submit_rope(Dataflow_Handle * handle, int stream_id,
+						DataflowDatatype fwd_dt,
+						uint64_t N, int model_dim, int head_dim, int num_kv_heads, int theta,
+						int * seq_positions, void * X_q, void * X_k);
+
+/* In-place inverse (transposed) rotation of dX_q and dX_k. */
+int submit_rope_bwd_x(Dataflow_Handle * handle, int stream_id,
+						DataflowDatatype bwd_dt,
+						uint64_t N, int model_dim, int head_dim, int num_kv_heads, int theta,
+						int * seq_positions, void * dX_q, void * dX_k);
+
+/* --- mlp misc (reference: src/dataflow_ops/src/mlp_misc_ops.c:3-61) --- */
+
+/* out = silu(x_w1) * x_w3 */
+int submit_swiglu(Dataflow_Handle * handle, int stream_id,
+						DataflowDatatype fwd_dt,
+						int num_rows, int num_cols,
+						void * x_w1, void * x_w3, void * out);
+
+/* dX_w3 = dOut * silu(x_w1); dX_w1 = dOut * x_w3 * silu'(x_w1) */
+int submit_swiglu_bwd_x(Dataflow_Handle * handle, int stream_id,
+						DataflowDatatype fwd_dt, DataflowDatatype bwd_dt,
+						int num_rows, int num_cols,
+						void * x_w1, void * x_w3,
+						void * upstream_dX, void * dX_w1, void * dX_w3);
+
+/* --- loss (reference: src/dataflow_ops/src/loss_misc_ops.c:4-60) --- */
+
+/* Row softmax of X (fwd_dt) into out (bwd_dt). */
+int submit_softmax(Dataflow_Handle * handle, int stream_id,
+						DataflowDatatype fwd_dt, DataflowDatatype bwd_dt,
+						int n_rows, int n_cols,
+						void * X, void * out);
+
+/* pred_logits[r, labels[r]] -= 1 in place (labels >= n_cols are skipped). */
+int submit_cross_entropy_loss(Dataflow_Handle * handle, int stream_id,
+								DataflowDatatype bwd_dt,
+								int n_rows, int n_cols,
+								void * pred_logits, uint32_t * labels);
+
+/* Fused softmax + cross-entropy: per-row fp32 loss, fp32 mean loss, and the
+ * logits overwritten in place by softmax - onehot. No reference counterpart. */
+int submit_softmax_cross_entropy_loss(Dataflow_Handle * handle, int stream_id,
+								DataflowDatatype dt,
+								int n_rows, int n_cols,
+								void * logits, uint32_t * labels, float * loss, float * mean_loss);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif

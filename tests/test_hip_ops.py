@@ -1,0 +1,425 @@
+"""Parity of the gfx950 kernels (through the C ABI) with the oracle.
+
+Every op is called through libdataflow.so's submit_* entry points on an AMD GPU
+and compared with oracle/liboracle.so on the same seeded inputs, at sizes the
+oracle finishes in well under a second, across fp32/fp16/bf16, the vector
+and element paths (aligned, unaligned, ragged and over-long rows), and edge
+values. Criteria (tests/support.py): half-precision outputs within 1 ulp of
+the exact pre-rounding value (or the oracle's interval where the reference
+rounds intermediates, plus an fp32 evaluation-noise floor where the exact
+expression cancels); fp32 outputs within 1e-5 relative (ws/dW: plus 1e-6 of
+the sum of |terms|); losses within 1e-4 relative.
+"""
+import ctypes
+
+import numpy as np
+import pytest
+
+from support import (BF16, FP16, FP32, NP_STORAGE, check_f32, check_rounded, normal, oracle, ptr, rng, to_f64,
+                     to_storage)
+
+pytestmark = pytest.mark.gpu
+DTS = [FP32, FP16, BF16]
+DT_IDS = {FP32: "fp32", FP16: "fp16", BF16: "bf16"}
+
+
+@pytest.fixture(scope="module")
+def hdl():
+    from dataflow_lib_amd import api
+    h = api.Handle(0, num_streams=2)
+    yield h
+    h.destroy()
+
+
+class Dev:
+    """Device buffers of one test, freed at exit. `offset_bytes` shifts a
+    buffer off its 256-byte allocation alignment to exercise the element path."""
+
+    def __init__(self, h):
+        self.h, self.bufs = h, []
+
+    def __enter__(self):
+        return self
+
+    def put(self, arr, offset_bytes=0):
+        arr = np.ascontiguousarray(arr)
+        base = self.h.alloc(arr.nbytes + offset_bytes + 16)
+        self.bufs.append(base)
+        p = base + offset_bytes
+        self.h.to_device(arr, p)
+        return p
+
+    def empty(self, nbytes):
+        p = self.h.alloc(nbytes + 16)
+        self.bufs.append(p)
+        return p
+
+    def get(self, p, shape, dtype):
+        self.h.sync()
+        return self.h.to_host(p, shape, dtype)
+
+    def __exit__(self, *exc):
+        self.h.sync()
+        for p in self.bufs:
+            self.h.free(p)
+
+
+def dt_id(dt):
+    return DT_IDS[dt]
+
+
+# ---------------- RMSNorm ----------------
+
+RMS_SHAPES = [(16, 4096), (64, 4096), (7, 8192), (33, 1000), (5, 8), (3, 20000)]
+
+
+def rms_inputs(dt, n_rows, n_cols, seed=1):
+    X = to_storage(normal(seed, (n_rows, n_cols)), dt)
+    W = to_storage(1.0 + normal(seed + 1, (n_cols,), std=0.02), dt)
+    return X, W
+
+
+def oracle_rms(dt, X, W, eps):
+    n_rows, n_cols = X.shape
+    y = np.empty((n_rows, n_cols)), np.empty(n_rows), np.empty(n_rows), np.empty(n_rows)
+    assert oracle().oracle_rms_norm(dt, n_rows, n_cols, eps, ptr(W), ptr(X), *[ptr(a) for a in y]) == 0
+    return y
+
+
+@pytest.mark.parametrize("dt", DTS, ids=dt_id)
+@pytest.mark.parametrize("shape", RMS_SHAPES, ids=lambda s: "%dx%d" % s)
+def test_rms_norm_fwd(hdl, dt, shape):
+    from dataflow_lib_amd import api
+    n_rows, n_cols = shape
+    eps = 1e-5
+    X, W = rms_inputs(dt, n_rows, n_cols)
+    y_pre, ws, rs, ws_abs = oracle_rms(dt, X, W, eps)
+    with Dev(hdl) as d:
+        px, pw = d.put(X), d.put(W)
+        py, pws, prs = d.empty(X.nbytes), d.empty(4 * n_rows), d.empty(4 * n_rows)
+        assert api.submit_rms_norm(hdl, 0, dt, n_rows, n_cols, eps, pw, px, py, pws, prs) == 0
+        y = d.get(py, X.shape, NP_STORAGE[dt])
+        gws = d.get(pws, (n_rows,), np.float32)
+        grs = d.get(prs, (n_rows,), np.float32)
+    check_rounded(y, dt, y_pre, what="rms_norm y")
+    check_f32(grs, rs, what="rms_norm rstd")
+    check_f32(gws, ws, floor=1e-6 * ws_abs, what="rms_norm weighted_sums")
+
+
+@pytest.mark.parametrize("dt", [FP32, BF16], ids=dt_id)
+def test_rms_norm_fwd_unaligned_and_null_stats(hdl, dt):
+    """pointers off 16-byte alignment take the element path; NULL stats are skipped"""
+    from dataflow_lib_amd import api
+    n_rows, n_cols = 9, 4096
+    X, W = rms_inputs(dt, n_rows, n_cols, seed=5)
+    y_pre, _, _, _ = oracle_rms(dt, X, W, 1e-6)
+    with Dev(hdl) as d:
+        px, pw = d.put(X, offset_bytes=2 if dt != FP32 else 4), d.put(W)
+        py = d.empty(X.nbytes)
+        assert api.submit_rms_norm(hdl, 0, dt, n_rows, n_cols, 1e-6, pw, px, py, None, None) == 0
+        y = d.get(py, X.shape, NP_STORAGE[dt])
+    check_rounded(y, dt, y_pre, what="rms_norm unaligned y")
+
+
+def rms_bwd_inputs(dt, n_rows, n_cols, seed=11):
+    X, W = rms_inputs(dt, n_rows, n_cols, seed)
+    _, ws, rs, _ = oracle_rms(dt, X, W, 1e-5)
+    ws32, rs32 = ws.astype(np.float32), rs.astype(np.float32)
+    dY = to_storage(normal(seed + 2, (n_rows, n_cols)), dt)
+    dX = to_storage(normal(seed + 3, (n_rows, n_cols)), dt)
+    return X, W, ws32, rs32, dY, dX
+
+
+@pytest.mark.parametrize("dt", DTS, ids=dt_id)
+@pytest.mark.parametrize("shape", RMS_SHAPES, ids=lambda s: "%dx%d" % s)
+def test_rms_norm_bwd_x(hdl, dt, shape):
+    from dataflow_lib_amd import api
+    n_rows, n_cols = shape
+    X, W, ws, rs, dY, dX = rms_bwd_inputs(dt, n_rows, n_cols)
+    lo, hi = np.empty((n_rows, n_cols)), np.empty((n_rows, n_cols))
+    assert oracle().oracle_rms_norm_bwd_x(dt, n_rows, n_cols, ptr(ws), ptr(rs), ptr(W), ptr(X), ptr(dY), ptr(dX),
+                                          ptr(lo), ptr(hi)) == 0
+    with Dev(hdl) as d:
+        p = [d.put(a) for a in (ws, rs, W, X, dY, dX)]
+        assert api.submit_rms_norm_bwd_x(hdl, 0, dt, dt, n_rows, n_cols, 1e-5, *p) == 0
+        out = d.get(p[5], X.shape, NP_STORAGE[dt])
+    check_rounded(out, dt, lo, hi, what="rms_norm_bwd_x dX")
+
+
+@pytest.mark.parametrize("dt", DTS, ids=dt_id)
+@pytest.mark.parametrize("shape", RMS_SHAPES, ids=lambda s: "%dx%d" % s)
+def test_rms_norm_bwd_w(hdl, dt, shape):
+    from dataflow_lib_amd import api
+    n_rows, n_cols = shape
+    X, W, ws, rs, dY, _ = rms_bwd_inputs(dt, n_rows, n_cols)
+    dW = to_storage(normal(21, (n_cols,), std=0.1), dt)
+    pre, absum = np.empty(n_cols), np.empty(n_cols)
+    assert oracle().oracle_rms_norm_bwd_w(dt, dt, n_rows, n_cols, ptr(rs), ptr(X), ptr(dY), ptr(dW), ptr(pre), ptr(absum)) == 0
+    with Dev(hdl) as d:
+        prs, px, pdy, pdw = d.put(rs), d.put(X), d.put(dY), d.put(dW)
+        assert api.submit_rms_norm_bwd_w(hdl, 0, dt, dt, n_rows, n_cols, 1e-5, prs, px, pdy, pdw) == 0
+        out = d.get(pdw, (n_cols,), NP_STORAGE[dt])
+    check_rounded(out, dt, pre, floor=1e-6 * absum, what="rms_norm_bwd_w dW")
+
+
+@pytest.mark.parametrize("dt", DTS, ids=dt_id)
+@pytest.mark.parametrize("shape", RMS_SHAPES + [(300, 512)], ids=lambda s: "%dx%d" % s)
+def test_rms_norm_bwd_fused(hdl, dt, shape):
+    from dataflow_lib_amd import api
+    n_rows, n_cols = shape
+    X, W, ws, rs, dY, dX = rms_bwd_inputs(dt, n_rows, n_cols)
+    dW = normal(31, (n_cols,), std=0.1)
+    dx_pre, dx_floor = np.empty((n_rows, n_cols)), np.empty((n_rows, n_cols))
+    dw_pre, dw_abs = np.empty(n_cols), np.empty(n_cols)
+    assert oracle().oracle_rms_norm_bwd(dt, n_rows, n_cols, ptr(rs), ptr(W), ptr(X), ptr(dY), ptr(dX), ptr(dW),
+                                        ptr(dx_pre), ptr(dx_floor), ptr(dw_pre), ptr(dw_abs)) == 0
+    with Dev(hdl) as d:
+        prs, pw, px, pdy, pdx, pdw = d.put(rs), d.put(W), d.put(X), d.put(dY), d.put(dX), d.put(dW)
+        assert api.submit_rms_norm_bwd(hdl, 0, dt, dt, n_rows, n_cols, 1e-5, prs, pw, px, pdy, pdx, pdw) == 0
+        gdx = d.get(pdx, X.shape, NP_STORAGE[dt])
+        gdw = d.get(pdw, (n_cols,), np.float32)
+    check_rounded(gdx, dt, dx_pre, floor=dx_floor, what="rms_norm_bwd dX")
+    check_f32(gdw, dw_pre, floor=1e-6 * dw_abs, what="rms_norm_bwd dW")
+
+
+def test_rms_norm_bwd_repeat_is_deterministic(hdl):
+    """two-pass dW: repeated launches (shared scratch, partial count) give identical bits"""
+    from dataflow_lib_amd import api
+    dt, n_rows, n_cols = BF16, 1000, 4096
+    X, W, ws, rs, dY, dX = rms_bwd_inputs(dt, n_rows, n_cols, seed=41)
+    outs = []
+    with Dev(hdl) as d:
+        prs, pw, px, pdy = d.put(rs), d.put(W), d.put(X), d.put(dY)
+        for _ in range(3):
+            pdx, pdw = d.put(dX), d.put(np.zeros(n_cols, np.float32))
+            assert api.submit_rms_norm_bwd(hdl, 0, dt, dt, n_rows, n_cols, 1e-5, prs, pw, px, pdy, pdx, pdw) == 0
+            outs.append((d.get(pdx, X.shape, np.uint16), d.get(pdw, (n_cols,), np.float32)))
+        # a smaller launch in between must not leave stale partials behind
+        pdw_small = d.put(np.zeros(n_cols, np.float32))
+        assert api.submit_rms_norm_bwd_w(hdl, 0, dt, dt, 3, n_cols, 1e-5, prs, px, pdy, d.put(np.zeros(n_cols, np.uint16))) == 0
+        pdx = d.put(dX)
+        assert api.submit_rms_norm_bwd(hdl, 0, dt, dt, n_rows, n_cols, 1e-5, prs, pw, px, pdy, pdx, pdw_small) == 0
+        outs.append((d.get(pdx, X.shape, np.uint16), d.get(pdw_small, (n_cols,), np.float32)))
+    for a, b in outs[1:]:
+        assert np.array_equal(a, outs[0][0]) and np.array_equal(b.view(np.uint32), outs[0][1].view(np.uint32))
+
+
+# ---------------- RoPE ----------------
+
+ROPE_CASES = [  # (tokens, q_heads, kv_heads, head_dim, theta)
+    (64, 32, 8, 128, 500000),
+    (17, 4, 2, 64, 10000),
+    (9, 3, 1, 96, 500000),
+    (5, 2, 2, 6, 10000),
+    (3, 2, 0, 128, 500000),
+]
+
+
+def rope_inputs(dt, T, nq, nkv, hd, seed=51):
+    Q = to_storage(normal(seed, (T, nq * hd)), dt)
+    K = to_storage(normal(seed + 1, (T, nkv * hd)), dt)
+    pos = rng(seed + 2).integers(0, 2048, size=T).astype(np.int32)
+    pos[0] = 0
+    if T > 2:
+        pos[-1] = 131071
+    return Q, K, pos
+
+
+@pytest.mark.parametrize("bwd", [0, 1], ids=["fwd", "bwd"])
+@pytest.mark.parametrize("dt", DTS, ids=dt_id)
+@pytest.mark.parametrize("case", ROPE_CASES, ids=lambda c: "T%d_q%d_kv%d_hd%d" % c[:4])
+def test_rope(hdl, dt, case, bwd):
+    from dataflow_lib_amd import api
+    T, nq, nkv, hd, theta = case
+    Q, K, pos = rope_inputs(dt, T, nq, nkv, hd)
+    N = T * nq * hd
+    qv, kv = np.empty(Q.shape), np.empty(K.shape)
+    assert oracle().oracle_rope(dt, bwd, N, nq * hd, hd, nkv, theta, ptr(pos), ptr(Q), ptr(K), ptr(qv), ptr(kv)) == 0
+    with Dev(hdl) as d:
+        pq, pk, pp = d.put(Q), d.put(K), d.put(pos)
+        fn = api.submit_rope_bwd_x if bwd else api.submit_rope
+        assert fn(hdl, 0, dt, N, nq * hd, hd, nkv, theta, pp, pq, pk) == 0
+        gq = d.get(pq, Q.shape, NP_STORAGE[dt])
+        gk = d.get(pk, K.shape, NP_STORAGE[dt])
+    check_rounded(gq, dt, qv, what="rope Q")
+    if K.size:
+        check_rounded(gk, dt, kv, what="rope K")
+
+
+def test_rope_unaligned(hdl):
+    from dataflow_lib_amd import api
+    dt, T, nq, nkv, hd, theta = BF16, 6, 4, 2, 128, 500000
+    Q, K, pos = rope_inputs(dt, T, nq, nkv, hd, seed=61)
+    N = T * nq * hd
+    qv, kv = np.empty(Q.shape), np.empty(K.shape)
+    assert oracle().oracle_rope(dt, 0, N, nq * hd, hd, nkv, theta, ptr(pos), ptr(Q), ptr(K), ptr(qv), ptr(kv)) == 0
+    with Dev(hdl) as d:
+        pq, pk, pp = d.put(Q, offset_bytes=4), d.put(K), d.put(pos)
+        assert api.submit_rope(hdl, 0, dt, N, nq * hd, hd, nkv, theta, pp, pq, pk) == 0
+        gq, gk = d.get(pq, Q.shape, np.uint16), d.get(pk, K.shape, np.uint16)
+    check_rounded(gq, dt, qv, what="rope unaligned Q")
+    check_rounded(gk, dt, kv, what="rope unaligned K")
+
+
+def test_rope_rejects_bad_shapes(hdl):
+    from dataflow_lib_amd import api
+    with Dev(hdl) as d:
+        p = d.empty(4096)
+        assert api.submit_rope(hdl, 0, BF16, 100, 64, 64, 1, 10000, p, p, p) == -1      # N not a multiple of model_dim
+        assert api.submit_rope(hdl, 0, BF16, 128, 64, 7, 1, 10000, p, p, p) == -1       # odd head_dim
+        assert api.submit_rope(hdl, 0, BF16, 2048, 1024, 1024, 1, 10000, p, p, p) == -1  # head_dim > 512
+
+
+# ---------------- SwiGLU ----------------
+
+SWIGLU_SHAPES = [(33, 1000), (8, 14336), (1, 7), (3, 5)]
+
+
+def swiglu_inputs(dt, shape, seed=71, extremes=False):
+    g32 = normal(seed, shape, std=2.0)
+    u32 = normal(seed + 1, shape)
+    d32 = normal(seed + 2, shape)
+    if extremes:
+        flat = g32.ravel()
+        vals = np.array([0.0, -0.0, 88.0, -88.0, -89.0, 100.0, -100.0, 1e4, -1e4, -1.2785, 30.0, -30.0], np.float32)
+        flat[:vals.size] = vals
+    return to_storage(g32, dt), to_storage(u32, dt), to_storage(d32, dt)
+
+
+@pytest.mark.parametrize("dt", DTS, ids=dt_id)
+@pytest.mark.parametrize("shape", SWIGLU_SHAPES, ids=lambda s: "%dx%d" % s)
+def test_swiglu_fwd(hdl, dt, shape):
+    from dataflow_lib_amd import api
+    g, u, _ = swiglu_inputs(dt, shape, extremes=(shape[1] > 12))
+    n = g.size
+    pre = np.empty(shape)
+    assert oracle().oracle_swiglu(dt, n, ptr(g), ptr(u), ptr(pre)) == 0
+    with Dev(hdl) as d:
+        pg, pu, po = d.put(g), d.put(u), d.empty(g.nbytes)
+        assert api.submit_swiglu(hdl, 0, dt, shape[0], shape[1], pg, pu, po) == 0
+        out = d.get(po, shape, NP_STORAGE[dt])
+    check_rounded(out, dt, pre, what="swiglu out")
+
+
+@pytest.mark.parametrize("dt", DTS, ids=dt_id)
+@pytest.mark.parametrize("shape", SWIGLU_SHAPES, ids=lambda s: "%dx%d" % s)
+def test_swiglu_bwd(hdl, dt, shape):
+    from dataflow_lib_amd import api
+    g, u, dO = swiglu_inputs(dt, shape, seed=81, extremes=(shape[1] > 12))
+    n = g.size
+    dg, dgf, du = np.empty(shape), np.empty(shape), np.empty(shape)
+    assert oracle().oracle_swiglu_bwd(dt, n, ptr(g), ptr(u), ptr(dO), ptr(dg), ptr(dgf), ptr(du)) == 0
+    with Dev(hdl) as d:
+        pg, pu, pd = d.put(g), d.put(u), d.put(dO)
+        pdg, pdu = d.empty(g.nbytes), d.empty(g.nbytes)
+        assert api.submit_swiglu_bwd_x(hdl, 0, dt, dt, shape[0], shape[1], pg, pu, pd, pdg, pdu) == 0
+        gdg, gdu = d.get(pdg, shape, NP_STORAGE[dt]), d.get(pdu, shape, NP_STORAGE[dt])
+    check_rounded(gdu, dt, du, what="swiglu dU")
+    check_rounded(gdg, dt, dg, floor=dgf, what="swiglu dG")
+    assert not np.isnan(to_f64(gdg, dt)).any(), "dG must stay finite for very negative gates"
+
+
+def test_swiglu_unaligned(hdl):
+    from dataflow_lib_amd import api
+    dt, shape = BF16, (4, 1003)
+    g, u, _ = swiglu_inputs(dt, shape, seed=91)
+    pre = np.empty(shape)
+    assert oracle().oracle_swiglu(dt, g.size, ptr(g), ptr(u), ptr(pre)) == 0
+    with Dev(hdl) as d:
+        pg, pu, po = d.put(g, offset_bytes=6), d.put(u), d.empty(g.nbytes)
+        assert api.submit_swiglu(hdl, 0, dt, shape[0], shape[1], pg, pu, po) == 0
+        out = d.get(po, shape, np.uint16)
+    check_rounded(out, dt, pre, what="swiglu unaligned")
+
+
+# ---------------- softmax / cross-entropy ----------------
+
+SMX_SHAPES = [(4, 128256), (3, 1000), (2, 1001), (2, 140000), (5, 64), (1, 1)]
+
+
+def logits(dt, shape, seed=101):
+    x = normal(seed, shape, std=2.0)
+    if shape[1] >= 16:
+        x[0, 3] = -np.inf
+        x[-1, 5] = 30.0
+    return to_storage(x, dt)
+
+
+@pytest.mark.parametrize("dt", DTS, ids=dt_id)
+@pytest.mark.parametrize("shape", SMX_SHAPES, ids=lambda s: "%dx%d" % s)
+def test_softmax(hdl, dt, shape):
+    from dataflow_lib_amd import api
+    n_rows, n_cols = shape
+    X = logits(dt, shape)
+    pre = np.empty(shape)
+    assert oracle().oracle_softmax(dt, dt, n_rows, n_cols, ptr(X), ptr(pre)) == 0
+    with Dev(hdl) as d:
+        px, po = d.put(X), d.empty(X.nbytes)
+        assert api.submit_softmax(hdl, 0, dt, dt, n_rows, n_cols, px, po) == 0
+        out = d.get(po, shape, NP_STORAGE[dt])
+    check_rounded(out, dt, pre, what="softmax")
+
+
+@pytest.mark.parametrize("dt", DTS, ids=dt_id)
+def test_cross_entropy_loss(hdl, dt):
+    from dataflow_lib_amd import api
+    n_rows, n_cols = 37, 1000
+    P = to_storage(rng(111).random((n_rows, n_cols)).astype(np.float32) / n_cols, dt)
+    labels = rng(112).integers(0, n_cols, size=n_rows).astype(np.uint32)
+    labels[0], labels[1], labels[2] = 0, n_cols - 1, n_cols + 5   # first, last, out of range (skipped)
+    expect = P.copy()
+    assert oracle().oracle_cross_entropy_loss(dt, n_rows, n_cols, ptr(expect), ptr(labels)) == 0
+    with Dev(hdl) as d:
+        pp, pl = d.put(P), d.put(labels)
+        assert api.submit_cross_entropy_loss(hdl, 0, dt, n_rows, n_cols, pp, pl) == 0
+        out = d.get(pp, P.shape, NP_STORAGE[dt])
+    assert np.array_equal(out.view(np.uint8), expect.view(np.uint8))
+
+
+@pytest.mark.parametrize("dt", DTS, ids=dt_id)
+@pytest.mark.parametrize("shape", SMX_SHAPES, ids=lambda s: "%dx%d" % s)
+def test_softmax_cross_entropy_fused(hdl, dt, shape):
+    from dataflow_lib_amd import api
+    n_rows, n_cols = shape
+    X = logits(dt, shape, seed=121)
+    labels = rng(122).integers(0, n_cols, size=n_rows).astype(np.uint32)
+    labels[0] = 0
+    if n_rows > 1:
+        labels[-1] = n_cols - 1
+    lo, hi, loss = np.empty(shape), np.empty(shape), np.empty(n_rows)
+    mean = np.zeros(1)
+    assert oracle().oracle_softmax_cross_entropy(dt, n_rows, n_cols, ptr(X), ptr(labels), ptr(lo), ptr(hi),
+                                                 ptr(loss), ptr(mean)) == 0
+    with Dev(hdl) as d:
+        for rep in range(2):   # the second run checks the mean-loss arrival counter was reset
+            px, pl = d.put(X), d.put(labels)
+            ploss, pmean = d.empty(4 * n_rows), d.empty(4)
+            assert api.submit_softmax_cross_entropy_loss(hdl, 0, dt, n_rows, n_cols, px, pl, ploss, pmean) == 0
+            out = d.get(px, shape, NP_STORAGE[dt])
+            gl = d.get(ploss, (n_rows,), np.float32)
+            gm = d.get(pmean, (1,), np.float32)
+            check_rounded(out, dt, lo, hi, what="fused dlogits")
+            check_f32(gl, loss, rel=1e-4, what="fused loss")
+            check_f32(gm, mean, rel=1e-4, what="fused mean loss")
+
+
+def test_softmax_cross_entropy_label_out_of_range(hdl):
+    from dataflow_lib_amd import api
+    dt, n_rows, n_cols = BF16, 3, 512
+    X = logits(dt, (n_rows, n_cols), seed=131)
+    labels = np.array([1, n_cols, 7], np.uint32)
+    with Dev(hdl) as d:
+        px, pl, ploss, pmean = d.put(X), d.put(labels), d.empty(12), d.empty(4)
+        assert api.submit_softmax_cross_entropy_loss(hdl, 0, dt, n_rows, n_cols, px, pl, ploss, pmean) == 0
+        gl = d.get(ploss, (n_rows,), np.float32)
+        gm = d.get(pmean, (1,), np.float32)
+    assert np.isfinite(gl[0]) and np.isnan(gl[1]) and np.isfinite(gl[2]) and np.isnan(gm[0])
+
+
+def test_unknown_variant_and_bad_stream(hdl):
+    from dataflow_lib_amd import api
+    with Dev(hdl) as d:
+        p = d.empty(1024)
+        # fp8 RMSNorm is a reference variant this library does not provide
+        assert api.submit_rms_norm(hdl, 0, api.DATAFLOW_FP8E4M3, 1, 16, 1e-5, p, p, p, None, None) == -1
+        assert api.submit_swiglu(hdl, 7, BF16, 1, 8, p, p, p) == -1
