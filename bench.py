@@ -330,6 +330,9 @@ def main():
     ap.add_argument("--no-extras", action="store_true")
     ap.add_argument("--cpu-budget", type=float, default=15.0, help="seconds of CPU baseline work")
     ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--copy-calibration", action="store_true",
+                    help="also run 4 device-to-device copies of 1 GiB (the HIP runtime's copy kernel), the known-size "
+                         "reference for scaling rocprofv3 FETCH_SIZE / WRITE_SIZE")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
         print("bench.py measures one GPU only: every GPU box here has a single MI355X and this build has no "
@@ -348,6 +351,11 @@ def main():
         print("bench: timing %d steps after %d warmup" % (args.steps, args.warmup), file=sys.stderr, flush=True)
         per_op, step_ms, wall = time_ops(h, hip, ops, args.steps, args.warmup)
         per_extra = time_ops(h, hip, extras, max(5, args.steps // 2), 1)[0] if extras else {}
+        if args.copy_calibration:
+            src, dst = pool.empty(GiB), pool.empty(GiB)
+            for _ in range(4):
+                assert h.copy(dst, src, GiB, 0) == 0
+            h.sync()
         info = h.device_info
         dev = {"arch": info.arch_name.decode(), "cu_count": info.cu_count, "num_xcds": info.num_xcds}
     finally:

@@ -176,8 +176,11 @@ int remove_table(Table * table, void * key, void * ret_value) {
 	}
 	/* backward-shift: pull later members of the chain into the hole when
 	 * their home slot does not lie cyclically in (hole, cur] */
-	uint64_t cur = (hole + 1) % size;
-	while (!slot_empty(table->is_empty_bit_vector, cur)) {
+	/* at most size - 1 slots follow the removed one (a full table has no
+	 * empty slot to stop at) */
+	for (uint64_t step = 1; step < size; step++) {
+		const uint64_t cur = ((uint64_t) found + step) % size;
+		if (slot_empty(table->is_empty_bit_vector, cur)) break;
 		uint8_t * cslot = slot_ptr(table, table->items, cur);
 		uint64_t home = table->config.hash_func(cslot, size);
 		bool home_in_gap = (hole <= cur) ? (home > hole && home <= cur) : (home > hole || home <= cur);
@@ -185,7 +188,6 @@ int remove_table(Table * table, void * key, void * ret_value) {
 			memcpy(slot_ptr(table, table->items, hole), cslot, slot_bytes(table));
 			hole = cur;
 		}
-		cur = (cur + 1) % size;
 	}
 	memset(slot_ptr(table, table->items, hole), 0, slot_bytes(table));
 	mark_empty(table->is_empty_bit_vector, hole);

@@ -30,6 +30,19 @@ enum RmsMode { RMS_FWD = 0, RMS_BWD_X = 1, RMS_BWD_W = 2, RMS_BWD = 3 };
 
 template <typename T> __device__ __forceinline__ float rnd_to(float f) { return to_f(from_f<T>(f)); }
 
+/* Reference formula of the X gradient (rms_norm_bwd_x.cu:245-252):
+ *   deriv = w*r - ((x*r^3)/n)*ws;  dX + rnd(dY * rnd(deriv))
+ * with rnd() the rounding to the storage type. Contraction is off here: for
+ * fp16 the compiler would otherwise narrow dY*t to an f16 multiply and fuse
+ * it with the add through the conversion, skipping the product's rounding. */
+template <typename T>
+__device__ __forceinline__ float bwd_x_elem(float w, float x, float dy, float dx, float r, float r3, float ws, int n_cols) {
+#pragma clang fp contract(off)
+	const float deriv = w * r - ((x * r3) / (float) n_cols) * ws;
+	const float p = rnd_to<T>(dy * rnd_to<T>(deriv));
+	return dx + p;
+}
+
 struct RmsArgs {
 	int n_rows, n_cols;
 	float eps;
@@ -152,10 +165,7 @@ __device__ __forceinline__ void rms_vector(const RmsArgs & a, int nv, float * ld
 						unpack16<T>(gr[c], gf);
 						unpack16<T>(drow[c * tpr + tr], df);
 #pragma unroll
-						for (int e = 0; e < V; e++) {
-							const float deriv = wf[e] * r - ((xf[e] * r3) / (float) n_cols) * ws;
-							df[e] = df[e] + rnd_to<T>(gf[e] * rnd_to<T>(deriv));
-						}
+						for (int e = 0; e < V; e++) df[e] = bwd_x_elem<T>(wf[e], xf[e], gf[e], df[e], r, r3, ws, n_cols);
 						drow[c * tpr + tr] = pack16<T>(df);
 					}
 				}
@@ -278,8 +288,7 @@ __device__ __forceinline__ void rms_stream(const RmsArgs & a, float * lds) {
 				const float ws = a.ws_in[row];
 				const float r3 = r * r * r;
 				for (int j = tr; j < n_cols; j += tpr) {
-					const float deriv = to_f(W[j]) * r - ((to_f(x[j]) * r3) / (float) n_cols) * ws;
-					yd[j] = from_f<T>(to_f(yd[j]) + rnd_to<T>(to_f(g[j]) * rnd_to<T>(deriv)));
+					yd[j] = from_f<T>(bwd_x_elem<T>(to_f(W[j]), to_f(x[j]), to_f(g[j]), to_f(yd[j]), r, r3, ws, n_cols));
 				}
 			}
 		}

@@ -23,6 +23,22 @@ __device__ __forceinline__ float sigmoidf_fast(float g) {
 	return __builtin_amdgcn_rcpf(1.0f + __builtin_amdgcn_exp2f(-g * LOG2E_F));
 }
 
+/* Below this gate value sigmoid(g) is under 2^-92 and the products are formed
+ * from exp(g) * 2^64 (a normal number down to g = -131) and scaled back at the
+ * end, so results that are normal fp32 numbers do not pass through an fp32
+ * subnormal (which the hardware reciprocal and exp2 flush to zero). */
+#define SWIGLU_DEEP_NEG (-64.0f)
+#define TWO_POW_M64 5.421010862427522e-20f
+
+__device__ __forceinline__ float exp_scaled64(float g) {   /* exp(g) * 2^64 */
+	return __builtin_amdgcn_exp2f(fmaf(g, LOG2E_F, 64.0f));
+}
+
+__device__ __forceinline__ float swiglu_fwd_elem(float g, float u) {
+	if (g < SWIGLU_DEEP_NEG) return ((g * u) * exp_scaled64(g)) * TWO_POW_M64;
+	return (g * sigmoidf_fast(g)) * u;
+}
+
 template <typename T>
 __device__ __forceinline__ void swiglu_fwd(long n, const T * g, const T * u, T * out) {
 	constexpr int VEC = VecOf<T>::N;
@@ -49,19 +65,25 @@ __device__ __forceinline__ void swiglu_fwd(long n, const T * g, const T * u, T *
 				unpack16<T>(gr[k], gf);
 				unpack16<T>(ur[k], uf);
 #pragma unroll
-				for (int e = 0; e < VEC; e++) of[e] = (gf[e] * sigmoidf_fast(gf[e])) * uf[e];
+				for (int e = 0; e < VEC; e++) of[e] = swiglu_fwd_elem(gf[e], uf[e]);
 				ov[v] = pack16<T>(of);
 			}
 		}
 	}
 	for (long i = nvec * VEC + tid; i < n; i += nth) {
-		const float gf = to_f(g[i]);
-		out[i] = from_f<T>((gf * sigmoidf_fast(gf)) * to_f(u[i]));
+		out[i] = from_f<T>(swiglu_fwd_elem(to_f(g[i]), to_f(u[i])));
 	}
 }
 
 template <typename T>
 __device__ __forceinline__ void swiglu_bwd_elem(float g, float u, float d, float & dg, float & du) {
+	if (g < SWIGLU_DEEP_NEG) {
+		/* sigmoid(g) = exp(g) to fp32 precision and 1 - sigmoid(g) = 1 */
+		const float e = exp_scaled64(g);
+		du = ((d * g) * e) * TWO_POW_M64;
+		dg = ((d * u) * (1.0f + g) * e) * TWO_POW_M64;
+		return;
+	}
 	const float s = sigmoidf_fast(g);
 	du = d * (g * s);
 	dg = d * (u * s * fmaf(g, 1.0f - s, 1.0f));

@@ -1,0 +1,104 @@
+"""The registry, fingerprint dispatch and argument marshalling of the product
+library, run end to end in a GPU-less process: register_native_ops() and the
+submit_* functions of libdataflow.so drive the CPU test backend in
+oracle/liboracle.so (COMPUTE_CPU), whose "<op>_<dt>_kernel" adapters read
+op_args exactly as the GPU kernels do. BASELINE config 1 (RMSNorm forward,
+fp32, 16 x 4096) runs here."""
+import ctypes
+
+import numpy as np
+import pytest
+
+from support import BF16, FP32, ORACLE_LIB, check_f32, normal, oracle, ptr, to_storage
+
+from dataflow_lib_amd import api
+
+
+@pytest.fixture(scope="module")
+def cpu_handle():
+    O = oracle()
+    O.init_cpu_dataflow_handle.argtypes = [ctypes.POINTER(api.DataflowHandle), ctypes.c_int]
+    O.destroy_cpu_dataflow_handle.argtypes = [ctypes.POINTER(api.DataflowHandle)]
+    h = api.DataflowHandle()
+    assert O.init_cpu_dataflow_handle(ctypes.byref(h), 2) == 0
+    n = api.lib().register_native_ops(ctypes.byref(h), ORACLE_LIB.encode(), b"")
+    yield h, n
+    O.destroy_cpu_dataflow_handle(ctypes.byref(h))
+
+
+def test_registers_every_variant(cpu_handle):
+    h, n = cpu_handle
+    assert n == 33 and h.num_ops == 33 and h.op_table.cnt == 33
+
+
+def test_config1_rms_norm_fp32_through_handle(cpu_handle):
+    """fp32 X [16 x 4096] ~ N(0,1), W = 1 + N(0, 0.02), eps 1e-5"""
+    h, _ = cpu_handle
+    n_rows, n_cols, eps = 16, 4096, 1e-5
+    X = normal(1, (n_rows, n_cols))
+    W = (1.0 + normal(2, (n_cols,), std=0.02)).astype(np.float32)
+    Y = np.empty_like(X)
+    ws, rs = np.empty(n_rows, np.float32), np.empty(n_rows, np.float32)
+    assert api.submit_rms_norm(ctypes.byref(h), 0, FP32, n_rows, n_cols, eps, ptr(W), ptr(X), ptr(Y), ptr(ws), ptr(rs)) == 0
+    y_pre, ws_e, rs_e, ws_abs = np.empty((n_rows, n_cols)), np.empty(n_rows), np.empty(n_rows), np.empty(n_rows)
+    assert oracle().oracle_rms_norm(FP32, n_rows, n_cols, eps, ptr(W), ptr(X), ptr(y_pre), ptr(ws_e), ptr(rs_e), ptr(ws_abs)) == 0
+    assert np.array_equal(Y, y_pre.astype(np.float32))
+    check_f32(rs, rs_e, rel=1e-7)
+    check_f32(ws, ws_e, rel=1e-7)
+    # closed form: mean_j (y/w)^2 = r^2 * ss/n = 1 - eps * r^2
+    assert np.allclose(((y_pre / W) ** 2).mean(axis=1), 1.0 - eps * rs_e ** 2, rtol=1e-12)
+
+
+def test_dispatch_uses_fingerprint_not_name(cpu_handle):
+    """an Op whose header differs only in one arg dtype must not resolve"""
+    h, _ = cpu_handle
+    op = api.Op()
+    op.op_skeleton = api.native_op_skeleton("swiglu", BF16)
+    op.op_skeleton.header.arg_dtypes[4] = FP32
+    api.lib().do_fingerprinting(ctypes.byref(op.op_skeleton.header), ctypes.sizeof(api.OpSkeletonHeader),
+                                op.op_skeleton.fingerprint, 0)
+    submit = ctypes.cast(h.submit_op, ctypes.CFUNCTYPE(ctypes.c_int, ctypes.POINTER(api.DataflowHandle),
+                                                       ctypes.POINTER(api.Op), ctypes.c_int))
+    assert submit(ctypes.byref(h), ctypes.byref(op), 0) == -1
+
+
+def test_error_paths(cpu_handle):
+    h, _ = cpu_handle
+    p = np.zeros(64, np.float32)
+    # unknown variant (fp8 is not provided) and an out-of-range stream id
+    assert api.submit_rms_norm(ctypes.byref(h), 0, api.DATAFLOW_FP8E4M3, 1, 16, 1e-5, ptr(p), ptr(p), ptr(p), None, None) == -1
+    assert api.submit_rms_norm(ctypes.byref(h), 5, FP32, 1, 16, 1e-5, ptr(p), ptr(p), ptr(p), None, None) == -1
+    assert api.submit_rms_norm(ctypes.byref(h), -1, FP32, 1, 16, 1e-5, ptr(p), ptr(p), ptr(p), None, None) == 0
+
+
+@pytest.mark.parametrize("op", ["swiglu", "softmax_xent", "rope", "rms_bwd"])
+def test_other_ops_through_handle(cpu_handle, op):
+    h, _ = cpu_handle
+    H = ctypes.byref(h)
+    if op == "swiglu":
+        g, u = to_storage(normal(3, (4, 64)), BF16), to_storage(normal(4, (4, 64)), BF16)
+        out = np.empty_like(g)
+        assert api.submit_swiglu(H, 0, BF16, 4, 64, ptr(g), ptr(u), ptr(out)) == 0
+        pre = np.empty((4, 64))
+        assert oracle().oracle_swiglu(BF16, g.size, ptr(g), ptr(u), ptr(pre)) == 0
+        from support import check_rounded
+        check_rounded(out, BF16, pre, what="cpu-dispatched swiglu")
+    elif op == "softmax_xent":
+        x = to_storage(normal(5, (3, 100), std=2.0), BF16)
+        lab = np.array([0, 50, 99], np.uint32)
+        loss, mean = np.empty(3, np.float32), np.empty(1, np.float32)
+        assert api.submit_softmax_cross_entropy_loss(H, 0, BF16, 3, 100, ptr(x), ptr(lab), ptr(loss), ptr(mean)) == 0
+        assert np.isfinite(loss).all() and abs(mean[0] - loss.mean()) < 1e-5
+    elif op == "rope":
+        q, k = to_storage(normal(6, (2, 256)), BF16), to_storage(normal(7, (2, 128)), BF16)
+        pos = np.array([0, 9], np.int32)
+        q0 = q.copy()
+        assert api.submit_rope(H, 0, BF16, 512, 256, 128, 1, 10000, ptr(pos), ptr(q), ptr(k)) == 0
+        assert np.array_equal(q[0], q0[0])     # position 0 is the identity rotation
+        assert not np.array_equal(q[1], q0[1])
+    else:
+        X = normal(8, (3, 32))
+        W, dY, dX = np.ones(32, np.float32), normal(9, (3, 32)), np.zeros((3, 32), np.float32)
+        rs, dW = np.ones(3, np.float32), np.zeros(32, np.float32)
+        assert api.submit_rms_norm_bwd(H, 0, FP32, FP32, 3, 32, 1e-5, ptr(rs), ptr(W), ptr(X), ptr(dY), ptr(dX), ptr(dW)) == 0
+        assert np.allclose(dW, (dY * X).sum(axis=0), rtol=1e-6)
