@@ -47,7 +47,9 @@ def oracle():
 
 
 def ptr(a):
-    return None if a is None else a.ctypes.data
+    """c_void_p to a numpy array's data; the pointer object keeps the array
+    alive, so temporaries survive until the C call returns"""
+    return None if a is None else a.ctypes.data_as(ctypes.c_void_p)
 
 
 # ---------------- formats ----------------

@@ -1,0 +1,299 @@
+"""Pins the C oracle (oracle/liboracle.so) before it is trusted as the checker.
+
+The reference publishes no golden vectors for these kernels and its tests
+assert nothing, so each oracle function is pinned by what the mathematics
+fixes, chosen so a dropped term, a wrong sign or a swapped operand fails:
+  rounding      - ties-to-even cases, grid membership, idempotence, fp32-bit RNE
+  rms_norm      - constant / zero rows, mean-square identity, numpy dot for ws
+  bwd (exact)   - central finite differences of the oracle's own forward
+  bwd_x (ref)   - equals the exact gradient when dY is constant along a row
+  bwd_w         - finite differences w.r.t. W
+  rope          - position 0 identity, c = 0 closed form, pair norms, bwd(fwd(x)) = x,
+                  2x2 rotation-matrix brute force
+  swiglu        - g = 0 values, finite differences, large-g limit
+  softmax / CE  - scipy softmax / logsumexp, constant rows, the bf16 rounding of
+                  x - max on a hand-computed row, label arithmetic
+"""
+import numpy as np
+import pytest
+from scipy.special import logsumexp, softmax as sp_softmax
+
+from support import BF16, FP16, FP32, bf16_bits_to_f32, f32_to_bf16_bits, normal, oracle, ptr, rng, to_f64, to_storage
+
+O = None
+
+
+def setup_module():
+    global O
+    O = oracle()
+
+
+# ---------------- rounding ----------------
+
+def test_round_ties_to_even_and_subnormals():
+    r = lambda v, dt: O.oracle_round(v, dt)
+    # bf16 has 8 significant bits: 1 + 2^-8 is halfway between 1 and 1 + 2^-7
+    assert r(1.0 + 2 ** -8, BF16) == 1.0
+    assert r(1.0 + 3 * 2 ** -8, BF16) == 1.0 + 2 ** -6
+    assert r(1.0 + 2 ** -8 + 2 ** -30, BF16) == 1.0 + 2 ** -7
+    assert r(-(1.0 + 2 ** -8), BF16) == -1.0
+    # fp16: 11 bits; fp32: 24 bits
+    assert r(1.0 + 2 ** -11, FP16) == 1.0 and r(1.0 + 3 * 2 ** -11, FP16) == 1.0 + 2 ** -9
+    assert r(1.0 + 2 ** -24, FP32) == 1.0 and r(1.0 + 3 * 2 ** -24, FP32) == 1.0 + 2 ** -22
+    # subnormal spacing: bf16 2^-133, fp16 2^-24; halfway ties go to the even multiple
+    assert r(1.5 * 2 ** -133, BF16) == 2 * 2 ** -133 and r(2.5 * 2 ** -133, BF16) == 2 * 2 ** -133
+    assert r(2.5 * 2 ** -24, FP16) == 2 * 2 ** -24 and r(0.4 * 2 ** -24, FP16) == 0.0
+    # overflow
+    assert r(65520.0, FP16) == np.inf and r(65519.0, FP16) == 65504.0
+    assert np.isinf(r(3.4e38 * 1.01, BF16))
+
+
+def test_round_matches_independent_conversions():
+    g = rng(1)
+    v = np.concatenate([g.standard_normal(2000) * 10.0 ** g.integers(-30, 30, 2000),
+                        g.standard_normal(500) * 1e-40, g.standard_normal(500) * 60000])
+    for x in v:
+        assert O.oracle_round(x, FP32) == float(np.float32(x))
+        assert O.oracle_round(x, FP16) == float(np.float16(x))
+    # bf16 of fp32-representable values: integer RNE on the fp32 bit pattern
+    f = v.astype(np.float32)
+    f = f[np.isfinite(f)]
+    want = bf16_bits_to_f32(f32_to_bf16_bits(f)).astype(np.float64)
+    got = np.array([O.oracle_round(float(x), BF16) for x in f])
+    assert np.array_equal(got, want)
+
+
+def test_round_is_on_grid_nearest_and_idempotent():
+    g = rng(2)
+    for x in g.standard_normal(3000) * 10.0 ** g.integers(-20, 20, 3000):
+        b = O.oracle_round(x, BF16)
+        assert O.oracle_round(b, BF16) == b
+        assert (np.float32(b).view(np.uint32) & 0xFFFF) == 0
+        assert abs(b - x) <= 0.5 * O.oracle_ulp(x, BF16) * (1 + 1e-12)
+
+
+# ---------------- RMSNorm ----------------
+
+def rmsf(dt, X, W, eps):
+    n_rows, n_cols = X.shape
+    y, ws, rs, wa = np.empty(X.shape), np.empty(n_rows), np.empty(n_rows), np.empty(n_rows)
+    assert O.oracle_rms_norm(dt, n_rows, n_cols, eps, ptr(W), ptr(X), ptr(y), ptr(ws), ptr(rs), ptr(wa)) == 0
+    return y, ws, rs
+
+
+def test_rms_norm_closed_forms():
+    n, eps = 64, 1e-5
+    X = np.zeros((3, n), np.float32)
+    X[0] = 0.75
+    X[2] = normal(3, (n,))
+    W = (1 + normal(4, (n,), std=0.1)).astype(np.float32)
+    y, ws, rs = rmsf(FP32, X, W, eps)
+    e32 = float(np.float32(eps))     # eps is an fp32 kernel argument
+    assert np.allclose(y[0], W.astype(np.float64) * 0.75 / np.sqrt(0.75 ** 2 + e32), rtol=1e-14)
+    assert np.all(y[1] == 0) and rs[1] == pytest.approx(1 / np.sqrt(e32), rel=1e-14)
+    assert ((y[2] / W.astype(np.float64)) ** 2).mean() == pytest.approx(1 - e32 * rs[2] ** 2, rel=1e-12)
+    assert ws[2] == pytest.approx(np.dot(X[2].astype(np.float64), W.astype(np.float64)), rel=1e-12)
+    # bf16 storage reads the same numbers
+    yb, _, rsb = rmsf(BF16, to_storage(X, BF16), to_storage(W, BF16), eps)
+    assert rsb[0] == pytest.approx(rs[0], rel=1e-14)
+
+
+def fd_grad(f, x, h=1e-3):
+    """central differences of scalar f over every element of the fp32 array x"""
+    g = np.empty(x.shape)
+    flat = x.ravel()
+    for i in range(flat.size):
+        orig = flat[i]
+        xp, xm = np.float32(orig + h), np.float32(orig - h)
+        flat[i] = xp
+        fp = f()
+        flat[i] = xm
+        fm = f()
+        flat[i] = orig
+        g.flat[i] = (fp - fm) / (np.float64(xp) - np.float64(xm))
+    return g
+
+
+def test_rms_norm_bwd_exact_matches_finite_differences():
+    n_rows, n_cols, eps = 3, 16, 1e-5
+    X = normal(5, (n_rows, n_cols))
+    W = (1 + normal(6, (n_cols,), std=0.3)).astype(np.float32)
+    dY = normal(7, (n_rows, n_cols))
+    L = lambda: float((rmsf(FP32, X, W, eps)[0] * dY).sum())
+    gx, gw = fd_grad(L, X), fd_grad(L, W)
+    _, _, rs = rmsf(FP32, X, W, eps)
+    dx, dxf, dw, dwa = np.empty(X.shape), np.empty(X.shape), np.empty(n_cols), np.empty(n_cols)
+    zeros = np.zeros_like(X)
+    assert O.oracle_rms_norm_bwd(FP32, n_rows, n_cols, ptr(rs.astype(np.float32)), ptr(W), ptr(X), ptr(dY), ptr(zeros),
+                                 ptr(np.zeros(n_cols, np.float32)), ptr(dx), ptr(dxf), ptr(dw), ptr(dwa)) == 0
+    assert np.allclose(dx, gx, rtol=2e-5, atol=2e-6)
+    assert np.allclose(dw, gw, rtol=2e-5, atol=2e-6)
+    # bwd_w alone gives the same dW
+    dw2, dwa2 = np.empty(n_cols), np.empty(n_cols)
+    assert O.oracle_rms_norm_bwd_w(FP32, FP32, n_rows, n_cols, ptr(rs.astype(np.float32)), ptr(X), ptr(dY),
+                                   ptr(np.zeros(n_cols, np.float32)), ptr(dw2), ptr(dwa2)) == 0
+    assert np.allclose(dw2, gw, rtol=2e-5, atol=2e-6)
+
+
+def test_rms_norm_bwd_x_reference_formula():
+    """with dY constant along each row, the reference's bwd_x formula equals the exact gradient;
+    with a non-constant dY it does not (it is not the gradient, by design of the reference)"""
+    n_rows, n_cols, eps = 3, 16, 1e-5
+    X = normal(8, (n_rows, n_cols))
+    W = (1 + normal(9, (n_cols,), std=0.3)).astype(np.float32)
+    _, ws, rs = rmsf(FP32, X, W, eps)
+    for const in (True, False):
+        dY = np.repeat(normal(10, (n_rows, 1)), n_cols, axis=1) if const else normal(11, (n_rows, n_cols))
+        L = lambda: float((rmsf(FP32, X, W, eps)[0] * dY).sum())
+        gx = fd_grad(L, X)
+        lo, hi = np.empty(X.shape), np.empty(X.shape)
+        assert O.oracle_rms_norm_bwd_x(FP32, n_rows, n_cols, ptr(ws.astype(np.float32)), ptr(rs.astype(np.float32)),
+                                       ptr(W), ptr(X), ptr(dY), ptr(np.zeros_like(X)), ptr(lo), ptr(hi)) == 0
+        assert np.allclose(lo, gx, rtol=1e-4, atol=1e-5) == const
+        assert np.all(np.abs(hi - lo) <= 1e-6 * (1 + np.abs(lo)))
+
+
+def test_rms_norm_bwd_x_half_precision_chain_brackets_fp32():
+    """the bf16 chain rounds deriv, the product and the sum: its value stays
+    within those three roundings of the fp32 result and dX_in carries through"""
+    n_rows, n_cols = 2, 32
+    X = to_storage(normal(12, (n_rows, n_cols)), BF16)
+    W = to_storage(1 + normal(13, (n_cols,), std=0.1), BF16)
+    dY = to_storage(normal(14, (n_rows, n_cols)), BF16)
+    dX = to_storage(normal(15, (n_rows, n_cols)), BF16)
+    _, ws, rs = rmsf(BF16, X, W, 1e-5)
+    args = [ptr(ws.astype(np.float32)), ptr(rs.astype(np.float32)), ptr(W), ptr(X), ptr(dY), ptr(dX)]
+    lo, hi = np.empty((n_rows, n_cols)), np.empty((n_rows, n_cols))
+    assert O.oracle_rms_norm_bwd_x(BF16, n_rows, n_cols, *args, ptr(lo), ptr(hi)) == 0
+    xf, wf, gf, df = (to_f64(a, BF16) for a in (X, W, dY, dX))
+    deriv = wf * rs[:, None] - (xf * rs[:, None] ** 3 / n_cols) * ws[:, None]
+    exact = df + gf * deriv
+    bound = np.abs(gf) * np.abs(deriv) * 2 ** -7 + np.abs(gf * deriv) * 2 ** -8
+    assert np.all(np.abs(lo - exact) <= bound + 1e-12)
+
+
+# ---------------- RoPE ----------------
+
+def rope(dt, bwd, Q, K, pos, hd, nkv, theta):
+    T = Q.shape[0]
+    qv, kv = np.empty(Q.shape), np.empty(K.shape)
+    assert O.oracle_rope(dt, bwd, Q.size, Q.shape[1], hd, nkv, theta, ptr(pos), ptr(Q), ptr(K), ptr(qv), ptr(kv)) == 0
+    return qv, kv
+
+
+def test_rope_closed_forms():
+    hd, nq, nkv, theta = 8, 2, 1, 10000
+    T = 4
+    Q, K = normal(20, (T, nq * hd)), normal(21, (T, nkv * hd))
+    pos = np.array([0, 1, 7, 1000], np.int32)
+    qv, kv = rope(FP32, 0, Q, K, pos, hd, nkv, theta)
+    assert np.array_equal(qv[0], Q[0].astype(np.float64)) and np.array_equal(kv[0], K[0].astype(np.float64))
+    # pair column 0 of each head turns by exactly (float) pos radians (angle = theta^0 = 1)
+    for t in range(T):
+        c, s = np.float32(np.cos(np.float64(np.float32(pos[t])))), np.float32(np.sin(np.float64(np.float32(pos[t]))))
+        for h in range(nq):
+            e, o = np.float64(Q[t, h * hd]), np.float64(Q[t, h * hd + 1])
+            assert qv[t, h * hd] == pytest.approx(c * e - s * o, rel=1e-15, abs=1e-15)
+            assert qv[t, h * hd + 1] == pytest.approx(c * o + s * e, rel=1e-15, abs=1e-15)
+    # pair norms are preserved
+    n0 = Q.astype(np.float64).reshape(T, -1, 2)
+    n1 = qv.reshape(T, -1, 2)
+    assert np.allclose((n1 ** 2).sum(-1), (n0 ** 2).sum(-1), rtol=1e-6)
+
+
+def test_rope_bruteforce_rotation_matrix_and_inverse():
+    hd, nq, nkv, theta = 4, 1, 1, 10000
+    Q, K = normal(22, (3, hd)), normal(23, (3, hd))
+    pos = np.array([3, 17, 250], np.int32)
+    qv, _ = rope(FP32, 0, Q, K, pos, hd, nkv, theta)
+    for t in range(3):
+        for p in range(hd // 2):
+            ang = np.float32(np.power(np.float64(theta), np.float64(np.float32(-(np.float32(2 * p) / np.float32(hd))))))
+            arg = np.float32(np.float32(pos[t]) * ang)
+            c, s = np.float32(np.cos(np.float64(arg))), np.float32(np.sin(np.float64(arg)))
+            R = np.array([[c, -s], [s, c]], np.float64)
+            want = R @ Q[t, 2 * p:2 * p + 2].astype(np.float64)
+            assert np.allclose(qv[t, 2 * p:2 * p + 2], want, rtol=1e-14, atol=1e-14)
+    # backward applies the transpose: bwd(fwd(x)) = x up to the fp32 storage of fwd(x)
+    q1 = qv.astype(np.float32)
+    k1 = np.zeros_like(K)
+    back, _ = rope(FP32, 1, q1, k1, pos, hd, nkv, theta)
+    assert np.allclose(back, Q, rtol=1e-6, atol=1e-6)
+
+
+# ---------------- SwiGLU ----------------
+
+def sw(dt, g, u, dO):
+    out, dg, dgf, du = np.empty(g.shape), np.empty(g.shape), np.empty(g.shape), np.empty(g.shape)
+    assert O.oracle_swiglu(dt, g.size, ptr(g), ptr(u), ptr(out)) == 0
+    assert O.oracle_swiglu_bwd(dt, g.size, ptr(g), ptr(u), ptr(dO), ptr(dg), ptr(dgf), ptr(du)) == 0
+    return out, dg, du
+
+
+def test_swiglu_closed_forms_and_finite_differences():
+    g = np.array([0.0, 0.0, 30.0, -3.0, 1.5, -800.0], np.float32)
+    u = np.array([2.0, -3.0, 1.5, 0.5, -1.25, 2.0], np.float32)
+    dO = np.array([1.0, 2.0, 1.0, 1.0, 1.0, 1.0], np.float32)
+    out, dg, du = sw(FP32, g, u, dO)
+    assert out[0] == 0 and du[0] == 0 and dg[0] == pytest.approx(1.0) and dg[1] == pytest.approx(3.0 * -1.0)
+    assert out[2] == pytest.approx(30.0 * 1.5, rel=1e-12)
+    assert np.isfinite(dg).all() and abs(dg[5]) < 1e-300
+    ones = np.ones_like(g)
+    gg = g[1:5].copy()
+    uu = u[1:5].copy()
+    fwd = lambda: float(sw(FP32, gg, uu, ones[1:5])[0].sum())
+    fd = fd_grad(fwd, gg, h=1e-3)
+    _, dg1, du1 = sw(FP32, gg, uu, ones[1:5])
+    assert np.allclose(dg1, fd, rtol=1e-5)
+    assert np.allclose(du1, sw(FP32, gg, ones[1:5], ones[1:5])[0], rtol=1e-14)
+
+
+# ---------------- softmax / cross-entropy ----------------
+
+def test_softmax_matches_scipy_and_sums_to_one():
+    X = normal(30, (4, 257), std=3.0)
+    y = np.empty(X.shape)
+    assert O.oracle_softmax(FP32, FP32, 4, 257, ptr(X), ptr(y)) == 0
+    assert np.allclose(y, sp_softmax(X.astype(np.float64), axis=1), rtol=1e-6)
+    assert np.allclose(y.sum(1), 1.0, rtol=1e-14)
+    c = np.full((1, 50), 2.5, np.float32)
+    yc = np.empty(c.shape)
+    assert O.oracle_softmax(FP32, FP32, 1, 50, ptr(c), ptr(yc)) == 0
+    assert np.allclose(yc, 1 / 50, rtol=1e-15)
+
+
+def test_softmax_rounds_x_minus_max_to_the_input_type():
+    # max 3; 2^-8 - 3 = -2.99609375 is not a bf16 value: it rounds to -3.0
+    x32 = np.array([[3.0, 2 ** -8]], np.float32)
+    yb = np.empty((1, 2))
+    assert O.oracle_softmax(BF16, BF16, 1, 2, ptr(to_storage(x32, BF16)), ptr(yb)) == 0
+    e = np.exp(-3.0)
+    assert yb[0, 0] == pytest.approx(1 / (1 + e), rel=1e-15) and yb[0, 1] == pytest.approx(e / (1 + e), rel=1e-15)
+    yf = np.empty((1, 2))
+    assert O.oracle_softmax(FP32, FP32, 1, 2, ptr(x32), ptr(yf)) == 0
+    ef = np.exp(2 ** -8 - 3.0)
+    assert yf[0, 1] == pytest.approx(ef / (1 + ef), rel=1e-12) and yf[0, 1] != yb[0, 1]
+
+
+def test_cross_entropy_and_fused_loss():
+    n_rows, n_cols = 5, 300
+    X = to_storage(normal(31, (n_rows, n_cols), std=2.0), BF16)
+    lab = np.array([0, 299, 17, 5, 400], np.uint32)   # the last is out of range
+    lo, hi, loss, mean = np.empty(X.shape), np.empty(X.shape), np.empty(n_rows), np.zeros(1)
+    assert O.oracle_softmax_cross_entropy(BF16, n_rows, n_cols, ptr(X), ptr(lab), ptr(lo), ptr(hi), ptr(loss), ptr(mean)) == 0
+    xf = to_f64(X, BF16)
+    for r in range(4):
+        assert loss[r] == pytest.approx(logsumexp(xf[r]) - xf[r, lab[r]], rel=1e-13)
+        assert -1.0 <= lo[r, lab[r]] <= hi[r, lab[r]] <= 0.0
+        assert abs(lo[r].sum()) < 2 ** -8     # softmax - onehot sums to zero up to the label rounding
+    assert np.isnan(loss[4]) and np.isnan(mean[0])
+    # constant row: loss = log n; dominant label: loss -> 0
+    C = to_storage(np.array([np.full(64, 1.5), np.r_[100.0, np.zeros(63)]], np.float32), BF16)
+    l2 = np.empty(2)
+    y2 = np.empty((2, 64))
+    assert O.oracle_softmax_cross_entropy(BF16, 2, 64, ptr(C), ptr(np.array([3, 0], np.uint32)), ptr(y2), None, ptr(l2), None) == 0
+    assert l2[0] == pytest.approx(np.log(64), rel=1e-14) and 0 <= l2[1] < 1e-40
+    # in-place label update of the split op: P - 1 in fp32, rounded to the storage type
+    P = to_storage(np.array([[0.25, 0.5], [0.125, 0.75]], np.float32), BF16)
+    assert O.oracle_cross_entropy_loss(BF16, 2, 2, ptr(P), ptr(np.array([1, 7], np.uint32))) == 0
+    assert np.array_equal(bf16_bits_to_f32(P), np.array([[0.25, -0.5], [0.125, 0.75]], np.float32))
