@@ -114,7 +114,7 @@ static int rms_dw_finish_config(Hip_Launch_Config * c, int n_rows, int n_cols) {
 		set_1d(c, 0, 1, 0);
 		return 0;
 	}
-	set_1d(c, (unsigned) MY_CEIL(n_cols, 256), 256, 0);
+	set_1d(c, (unsigned) MY_CEIL(n_cols, 64), RMS_FINISH_THREADS, 0);
 	return 0;
 }
 
@@ -187,9 +187,9 @@ static int swiglu_config(Hip_Launch_Config * c, Dataflow_Handle * h, Hip_Functio
 	}
 	const long n = (long) rows * (long) cols;
 	const long chunks = MY_CEIL(n, (long) (16 / elem));
-	long grid = MY_CEIL(chunks, 256L * SWIGLU_UNROLL);
-	grid = MY_MIN(grid, (long) dev(h)->cu_count * 16L);
-	set_1d(c, (unsigned) grid, 256, 0);
+	long grid = MY_CEIL(chunks, (long) SWIGLU_THREADS * SWIGLU_UNROLL);
+	grid = MY_MIN(grid, (long) dev(h)->cu_count * SWIGLU_WG_PER_CU);
+	set_1d(c, (unsigned) grid, SWIGLU_THREADS, 0);
 	return 0;
 }
 

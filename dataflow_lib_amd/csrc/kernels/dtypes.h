@@ -16,6 +16,8 @@ struct f16_t { uint16_t bits; };
 typedef __attribute__((ext_vector_type(2))) __bf16 bf16x2_v;
 typedef __attribute__((ext_vector_type(2))) _Float16 f16x2_v;
 
+typedef __attribute__((ext_vector_type(4))) uint32_t u32x4_v;
+
 /* one 16-byte memory vector */
 struct __attribute__((aligned(16))) R16 {
 	uint32_t w[4];
@@ -109,6 +111,19 @@ template <typename T> struct Chunk<T, 1> {
 
 __device__ __forceinline__ bool aligned16(const void * p) { return (((uintptr_t) p) & 15u) == 0; }
 
+/* 16-byte global accesses with the non-temporal hint, for data each kernel
+ * touches exactly once */
+__device__ __forceinline__ R16 ld16_nt(const void * p) {
+	const u32x4_v v = __builtin_nontemporal_load(reinterpret_cast<const u32x4_v *>(p));
+	R16 o;
+	o.w[0] = v.x; o.w[1] = v.y; o.w[2] = v.z; o.w[3] = v.w;
+	return o;
+}
+__device__ __forceinline__ void st16_nt(void * p, const R16 & x) {
+	const u32x4_v v = {x.w[0], x.w[1], x.w[2], x.w[3]};
+	__builtin_nontemporal_store(v, reinterpret_cast<u32x4_v *>(p));
+}
+
 /*
  * Raw buffer access: a 128-bit resource (base, byte range) in SGPRs, a
  * per-lane byte offset in one VGPR and a wave-uniform byte offset in an SGPR.
@@ -116,7 +131,6 @@ __device__ __forceinline__ bool aligned16(const void * p) { return (((uintptr_t)
  * tails need no branches. dword3 = 0x00020000 is the raw 32-bit data format
  * used by gfx9-family buffer instructions.
  */
-typedef __attribute__((ext_vector_type(4))) uint32_t u32x4_v;
 #define RAW_BUFFER_DWORD3 0x00020000
 
 __device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void * base, uint32_t num_bytes) {
@@ -131,4 +145,19 @@ __device__ __forceinline__ R16 buf_load16(__amdgpu_buffer_rsrc_t r, uint32_t vof
 __device__ __forceinline__ void buf_store16(__amdgpu_buffer_rsrc_t r, uint32_t voff, uint32_t soff, const R16 & x) {
 	const u32x4_v v = {x.w[0], x.w[1], x.w[2], x.w[3]};
 	__builtin_amdgcn_raw_buffer_store_b128(v, r, voff, soff, 0);
+}
+
+/* Non-temporal variants for data touched once (cache-policy bit 1: the
+ * streaming "nt" hint on gfx950), so single-use streams do not evict lines
+ * that other waves still reuse. */
+#define BUF_AUX_NT 2
+__device__ __forceinline__ R16 buf_load16_nt(__amdgpu_buffer_rsrc_t r, uint32_t voff, uint32_t soff) {
+	const u32x4_v v = __builtin_amdgcn_raw_buffer_load_b128(r, voff, soff, BUF_AUX_NT);
+	R16 o;
+	o.w[0] = v.x; o.w[1] = v.y; o.w[2] = v.z; o.w[3] = v.w;
+	return o;
+}
+__device__ __forceinline__ void buf_store16_nt(__amdgpu_buffer_rsrc_t r, uint32_t voff, uint32_t soff, const R16 & x) {
+	const u32x4_v v = {x.w[0], x.w[1], x.w[2], x.w[3]};
+	__builtin_amdgcn_raw_buffer_store_b128(v, r, voff, soff, BUF_AUX_NT);
 }

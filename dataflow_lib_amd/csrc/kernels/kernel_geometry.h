@@ -18,6 +18,8 @@
 #define RMS_STREAM_TPR 256
 /* LDS floats per row slot for the row reductions: [2 parities][32] */
 #define RMS_CELLS_PER_SLOT 64
+/* dW finish kernel: 64 columns per workgroup, partial rows spread over its waves */
+#define RMS_FINISH_THREADS 1024
 /* fp32 partial rows for the two-pass dW reduction (16 MiB) */
 #define RMS_DW_SCRATCH_FLOATS (4u << 20)
 
@@ -30,8 +32,11 @@
 #define ROPE_MAX_HEAD_DIM 512
 #define ROPE_WAVES 4
 
-/* SwiGLU: 16-byte chunks per thread in flight */
+/* SwiGLU: grid-stride, one 512-thread workgroup per CU, 16-byte chunks per
+ * thread in flight */
 #define SWIGLU_UNROLL 4
+#define SWIGLU_THREADS 512
+#define SWIGLU_WG_PER_CU 1
 
 #ifdef __HIPCC__
 #define GEOM_FN __host__ __device__ __forceinline__

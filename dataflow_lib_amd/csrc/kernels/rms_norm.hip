@@ -339,15 +339,39 @@ __device__ __forceinline__ void rms_run(const RmsArgs & a) {
 	else rms_stream<T, TW, MODE>(a, lds);
 }
 
-/* finish: dW[j] = rnd(dW[j] + sum_g partial[g][j]), partials in workgroup order */
+/* finish: dW[j] = rnd(dW[j] + sum_g partial[g][j]). A workgroup of
+ * RMS_FINISH_THREADS covers 64 consecutive columns (one per lane); wave w sums
+ * partial rows g = w, w + waves, ... (four loads in flight), and the wave sums
+ * are added in wave order, so the result does not depend on timing. */
 template <typename TW>
 __device__ __forceinline__ void rms_dw_finish(int n_cols, TW * dW) {
-	const int j = blockIdx.x * blockDim.x + threadIdx.x;
-	if (j >= n_cols) return;
+	__shared__ float wave_part[RMS_FINISH_THREADS / 64][64];
+	const int lane = threadIdx.x & 63;
+	const int wave = threadIdx.x >> 6;
+	const int nw = blockDim.x >> 6;
+	const int j = blockIdx.x * 64 + lane;
 	const int n_parts = g_rms_dw_nparts;
 	float s = 0.0f;
-	for (int g = 0; g < n_parts; g++) s += g_rms_dw_partials[(long) g * n_cols + j];
-	dW[j] = from_f<TW>(to_f(dW[j]) + s);
+	if (j < n_cols) {
+		const float * p = g_rms_dw_partials + j;
+		int g = wave;
+		for (; g + 3 * nw < n_parts; g += 4 * nw) {
+			const float a = p[(long) g * n_cols], b = p[(long) (g + nw) * n_cols];
+			const float c = p[(long) (g + 2 * nw) * n_cols], d = p[(long) (g + 3 * nw) * n_cols];
+			s += a;
+			s += b;
+			s += c;
+			s += d;
+		}
+		for (; g < n_parts; g += nw) s += p[(long) g * n_cols];
+	}
+	wave_part[wave][lane] = s;
+	__syncthreads();
+	if (wave == 0 && j < n_cols) {
+		float t = 0.0f;
+		for (int w = 0; w < nw; w++) t += wave_part[w][lane];
+		dW[j] = from_f<TW>(to_f(dW[j]) + t);
+	}
 }
 
 #define RMS_KERNELS(FSUF, PSUF, T)                                                                                       \
@@ -366,7 +390,7 @@ __device__ __forceinline__ void rms_dw_finish(int n_cols, TW * dW) {
 		RmsArgs a = {n_rows, n_cols, eps, nullptr, fwd_rms_vals, nullptr, nullptr, nullptr, X_inp, upstream_dX, nullptr, dW}; \
 		rms_run<T, T, RMS_BWD_W>(a);                                                                                     \
 	}                                                                                                                    \
-	extern "C" __global__ void __launch_bounds__(256) rms_norm_bwd_w_##PSUF##_kernel_finish(int n_rows, int n_cols,      \
+	extern "C" __global__ void __launch_bounds__(RMS_FINISH_THREADS) rms_norm_bwd_w_##PSUF##_kernel_finish(int n_rows, int n_cols,      \
 			float eps, float * fwd_rms_vals, T * X_inp, T * upstream_dX, T * dW) {                                      \
 		rms_dw_finish<T>(n_cols, dW);                                                                                    \
 	}                                                                                                                    \
@@ -375,7 +399,7 @@ __device__ __forceinline__ void rms_dw_finish(int n_cols, TW * dW) {
 		RmsArgs a = {n_rows, n_cols, eps, nullptr, fwd_rms_vals, nullptr, nullptr, rms_weight, X_inp, upstream_dX, dX, dW}; \
 		rms_run<T, float, RMS_BWD>(a);                                                                                   \
 	}                                                                                                                    \
-	extern "C" __global__ void __launch_bounds__(256) rms_norm_bwd_##PSUF##_kernel_finish(int n_rows, int n_cols,        \
+	extern "C" __global__ void __launch_bounds__(RMS_FINISH_THREADS) rms_norm_bwd_##PSUF##_kernel_finish(int n_rows, int n_cols,        \
 			float eps, float * fwd_rms_vals, T * rms_weight, T * X_inp, T * upstream_dX, T * dX, float * dW) {          \
 		rms_dw_finish<float>(n_cols, dW);                                                                                \
 	}

@@ -113,40 +113,27 @@ __device__ __forceinline__ void smx_regs(int n_rows, int n_cols, const T * X, TO
 		}
 
 		R16 xr[SMX_MAXCH];
-		/* max pass; the fused op also accumulates sx = sum exp(x - m_run)
-		 * against a running max, rescaled once per chunk */
 		float m = -__builtin_inff();
-		float sx = 0.0f;
 #pragma unroll
 		for (int c = 0; c < SMX_MAXCH; c++) {
 			if (c < nch) {
-				xr[c] = buf_load16(rin, voff, c * cstride);
+				xr[c] = buf_load16_nt(rin, voff, c * cstride);
 				float f[VEC];
 				unpack16<T>(xr[c], f);
 				float cm = f[0];
 #pragma unroll
 				for (int e = 1; e < VEC; e++) cm = fmaxf(cm, f[e]);
 				/* chunks past the row end hold zeros: keep them out of the max */
-				if (c * nt + tid >= nv) cm = -__builtin_inff();
-				if (FUSED) {
-					const float mn = fmaxf(m, cm);
-					if (cm != -__builtin_inff()) {
-						if (mn != m) sx *= exp_fast(m - mn);
-#pragma unroll
-						for (int e = 0; e < VEC; e++) sx += exp_fast(f[e] - mn);
-					}
-					m = mn;
-				}
-				else {
-					m = fmaxf(m, cm);
-				}
+				m = (c * nt + tid < nv) ? fmaxf(m, cm) : m;
 			}
 		}
-		const float m_thread = m;
 		m = block_max(m, slots);
-		if (FUSED) sx = (m_thread == -__builtin_inff()) ? 0.0f : sx * exp_fast(m_thread - m);
 
-		float sd = 0.0f;
+		/* sd = sum exp(d) with d = rnd(x - m); the fused op also needs
+		 * sx = sum exp(x - m) = sum exp(d) * exp(delta), delta = (x - m) - d
+		 * (exact in fp32, |delta| <= half an ulp of d), taken to first order:
+		 * the neglected e^d delta^2 / 2 terms change log(sx) by < 2e-6. */
+		float sd0 = 0.0f, sd1 = 0.0f, corr = 0.0f;
 #pragma unroll
 		for (int c = 0; c < SMX_MAXCH; c++) {
 			if (c < nch && c * nt + tid < nv) {
@@ -154,12 +141,18 @@ __device__ __forceinline__ void smx_regs(int n_rows, int n_cols, const T * X, TO
 				unpack16<T>(xr[c], f);
 #pragma unroll
 				for (int e = 0; e < VEC; e++) {
-					f[e] = rnd_in<T>(f[e] - m);
-					sd += exp_fast(f[e]);
+					const float diff = f[e] - m;
+					const float d = rnd_in<T>(diff);
+					const float ex = exp_fast(d);
+					if (e & 1) sd1 += ex; else sd0 += ex;
+					if (FUSED) corr = fmaf(ex, diff - d, corr);
+					f[e] = d;
 				}
 				xr[c] = pack16<T>(f);   /* d is exact in T */
 			}
 		}
+		float sd = sd0 + sd1;
+		float sx = sd + corr;
 		__syncthreads();   /* slots reuse */
 		block_sum2(sd, sx, slots);
 		const float inv = 1.0f / sd;
@@ -179,7 +172,7 @@ __device__ __forceinline__ void smx_regs(int n_rows, int n_cols, const T * X, TO
 					for (int e = 0; e < VEC; e++)
 						if (e == le) f[e] = rnd_in<TO>(f[e]) - 1.0f;
 				}
-				buf_store16(rout, voff, c * cstride, pack16<TO>(f));
+				buf_store16_nt(rout, voff, c * cstride, pack16<TO>(f));
 			}
 		}
 		if (FUSED && tid == 0 && loss) {

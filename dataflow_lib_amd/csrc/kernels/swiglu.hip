@@ -11,7 +11,10 @@
  * finite where the reference's form gives inf - inf = NaN (g < -88.7).
  *
  * Pure streaming: the [rows x cols] tensors are treated as flat arrays,
- * grid-stride over 16-byte chunks, four chunks per thread in flight.
+ * grid-stride over 16-byte chunks, four chunks per thread in flight, with
+ * non-temporal loads and stores. The launch uses one large workgroup per CU
+ * so that at any moment the whole GPU sweeps one compact window of memory,
+ * which is where gfx950's HBM sustains its highest mixed read/write rate.
  */
 #include "dtypes.h"
 #include "kernel_geometry.h"
@@ -55,7 +58,7 @@ __device__ __forceinline__ void swiglu_fwd(long n, const T * g, const T * u, T *
 #pragma unroll
 		for (int k = 0; k < SWIGLU_UNROLL; k++) {
 			const long v = v0 + k * nth;
-			if (v < nvec) { gr[k] = gv[v]; ur[k] = uv[v]; }
+			if (v < nvec) { gr[k] = ld16_nt(gv + v); ur[k] = ld16_nt(uv + v); }
 		}
 #pragma unroll
 		for (int k = 0; k < SWIGLU_UNROLL; k++) {
@@ -66,7 +69,7 @@ __device__ __forceinline__ void swiglu_fwd(long n, const T * g, const T * u, T *
 				unpack16<T>(ur[k], uf);
 #pragma unroll
 				for (int e = 0; e < VEC; e++) of[e] = swiglu_fwd_elem(gf[e], uf[e]);
-				ov[v] = pack16<T>(of);
+				st16_nt(ov + v, pack16<T>(of));
 			}
 		}
 	}
@@ -107,7 +110,7 @@ __device__ __forceinline__ void swiglu_bwd(long n, const T * g, const T * u, con
 #pragma unroll
 		for (int k = 0; k < SWIGLU_UNROLL; k++) {
 			const long v = v0 + k * nth;
-			if (v < nvec) { gr[k] = gv[v]; ur[k] = uv[v]; dr[k] = dv[v]; }
+			if (v < nvec) { gr[k] = ld16_nt(gv + v); ur[k] = ld16_nt(uv + v); dr[k] = ld16_nt(dv + v); }
 		}
 #pragma unroll
 		for (int k = 0; k < SWIGLU_UNROLL; k++) {
@@ -119,8 +122,8 @@ __device__ __forceinline__ void swiglu_bwd(long n, const T * g, const T * u, con
 				unpack16<T>(dr[k], df);
 #pragma unroll
 				for (int e = 0; e < VEC; e++) swiglu_bwd_elem<T>(gf[e], uf[e], df[e], ogf[e], ouf[e]);
-				dgv[v] = pack16<T>(ogf);
-				duv[v] = pack16<T>(ouf);
+				st16_nt(dgv + v, pack16<T>(ogf));
+				st16_nt(duv + v, pack16<T>(ouf));
 			}
 		}
 	}
@@ -133,11 +136,11 @@ __device__ __forceinline__ void swiglu_bwd(long n, const T * g, const T * u, con
 }
 
 #define SWIGLU_KERNELS(SUFFIX, BSUFFIX, T)                                                                           \
-	extern "C" __global__ void __launch_bounds__(256) swiglu_##SUFFIX##_kernel(int num_rows, int num_cols,          \
+	extern "C" __global__ void __launch_bounds__(512) swiglu_##SUFFIX##_kernel(int num_rows, int num_cols,          \
 			T * x_w1, T * x_w3, T * out) {                                                                           \
 		swiglu_fwd<T>((long) num_rows * (long) num_cols, x_w1, x_w3, out);                                           \
 	}                                                                                                                \
-	extern "C" __global__ void __launch_bounds__(256) swiglu_bwd_x_##BSUFFIX##_kernel(int num_rows, int num_cols,  \
+	extern "C" __global__ void __launch_bounds__(512) swiglu_bwd_x_##BSUFFIX##_kernel(int num_rows, int num_cols,  \
 			T * x_w1, T * x_w3, T * upstream_dX, T * dX_w1, T * dX_w3) {                                             \
 		swiglu_bwd<T>((long) num_rows * (long) num_cols, x_w1, x_w3, upstream_dX, dX_w1, dX_w3);                    \
 	}
