@@ -55,9 +55,10 @@ static int rms_check(const char * what, int n_rows, int n_cols, size_t elem) {
 /* rows per workgroup-iteration and grid for the row-streaming ops */
 static void rms_rowwise(Hip_Launch_Config * c, Dataflow_Handle * h, int n_rows, int nv) {
 	const int tpr = rms_tpr_for(nv);
-	const int per_cu = MY_MAX(1, 2048 / tpr);   /* ~32 waves of row slots per CU */
-	long grid = MY_MIN((long) n_rows, (long) dev(h)->cu_count * per_cu);
-	set_1d(c, (unsigned) grid, (unsigned) tpr, (unsigned) (RMS_CELLS_PER_SLOT * sizeof(float)));
+	/* two row slots per workgroup up to 512 threads, four workgroups per CU */
+	const int slots = MY_MAX(1, 512 / tpr);
+	long grid = MY_MIN((long) MY_CEIL(n_rows, slots), (long) dev(h)->cu_count * 4L);
+	set_1d(c, (unsigned) grid, (unsigned) (slots * tpr), (unsigned) (RMS_CELLS_PER_SLOT * slots * sizeof(float)));
 }
 
 int rms_norm_set_launch_config(Hip_Launch_Config * hip_launch_config, Dataflow_Handle * dataflow_handle, Hip_Function * hip_function, Op * op) {
@@ -161,7 +162,7 @@ static int rope_config(Hip_Launch_Config * c, Dataflow_Handle * h, Op * op, cons
 	}
 	const uint64_t n_tokens = N / (uint64_t) model_dim;
 	uint64_t grid = MY_CEIL(n_tokens, (uint64_t) ROPE_WAVES);
-	grid = MY_MIN(grid, (uint64_t) dev(h)->cu_count * 8u);
+	grid = MY_MIN(grid, (uint64_t) dev(h)->cu_count * 4u);
 	set_1d(c, (unsigned) grid, 64 * ROPE_WAVES, 0);
 	return 0;
 }
@@ -233,6 +234,15 @@ int softmax_cross_entropy_loss_set_launch_config(Hip_Launch_Config * hip_launch_
 		return -1;
 	}
 	return smx_config(hip_launch_config, hip_function, ARG(op, 0, int), ARG(op, 1, int), "softmax cross entropy loss");
+}
+
+int softmax_cross_entropy_loss_set_finish_launch_config(Hip_Launch_Config * hip_launch_config, Dataflow_Handle * dataflow_handle, Hip_Function * hip_function, Op * op) {
+	(void) dataflow_handle;
+	(void) hip_function;
+	const int n_rows = ARG(op, 0, int), n_cols = ARG(op, 1, int);
+	const int needed = n_rows > 0 && n_cols > 0 && ARG(op, 4, float *) && ARG(op, 5, float *);
+	set_1d(hip_launch_config, needed ? 1u : 0u, SMX_THREADS, 0);
+	return 0;
 }
 
 int cross_entropy_loss_set_launch_config(Hip_Launch_Config * hip_launch_config, Dataflow_Handle * dataflow_handle, Hip_Function * hip_function, Op * op) {

@@ -19,17 +19,15 @@
  * element is read from HBM once and written once. After the max pass the
  * registers are overwritten with d_j (exact in the storage type), so the
  * output pass needs no recomputation of x - m. exp uses the hardware exp2.
- * mean_loss is finished by the last workgroup to arrive (atomic ticket),
- * summing loss[] in row order, so it is deterministic.
+ * mean_loss is summed by a second kernel launched right after on the same
+ * stream (fixed order, fp64), so it is deterministic and needs no atomics or
+ * device-wide fences.
  */
 #include "dtypes.h"
 #include "reduce.h"
 #include "kernel_geometry.h"
 
 #define SMX_LOG2E 1.4426950408889634f
-
-/* arrival ticket for the mean-loss finish; reset by the last workgroup */
-__device__ unsigned int g_xent_arrivals;
 
 __device__ __forceinline__ float exp_fast(float x) { return __builtin_amdgcn_exp2f(x * SMX_LOG2E); }
 
@@ -60,21 +58,14 @@ __device__ __forceinline__ void block_sum2(float & a, float & b, float * slots) 
 	b = sb;
 }
 
-/* last workgroup to arrive sums loss[] in row order */
-__device__ __forceinline__ void finish_mean_loss(int n_rows, const float * loss, float * mean_loss, double * dslots) {
-	__shared__ int is_last;
-	__syncthreads();
-	if (threadIdx.x == 0) {
-		__threadfence();
-		const unsigned int prev = __hip_atomic_fetch_add(&g_xent_arrivals, 1u, __ATOMIC_ACQ_REL, __HIP_MEMORY_SCOPE_AGENT);
-		is_last = (prev == gridDim.x - 1) ? 1 : 0;
-	}
-	__syncthreads();
-	if (!is_last) return;
-	__threadfence();
+/* mean_loss = sum_r loss[r] / n_rows, summed in fp64 in a fixed order
+ * (thread t takes rows t, t + blockDim, ...; then the waves in order). Runs as
+ * the op's second kernel, after every row's loss is written. */
+__device__ __forceinline__ void mean_loss_finish(int n_rows, const float * loss, float * mean_loss) {
+	__shared__ double dslots[16];
+	if (blockIdx.x != 0 || !loss || !mean_loss) return;
 	double s = 0.0;
 	for (int r = threadIdx.x; r < n_rows; r += blockDim.x) s += (double) loss[r];
-	/* fixed-order tree over the 16 waves via LDS */
 	for (int off = 32; off > 0; off >>= 1) s += __shfl_xor(s, off);
 	if ((threadIdx.x & 63) == 0) dslots[threadIdx.x >> 6] = s;
 	__syncthreads();
@@ -82,7 +73,6 @@ __device__ __forceinline__ void finish_mean_loss(int n_rows, const float * loss,
 		double t = 0.0;
 		for (int w = 0; w < (int) (blockDim.x >> 6); w++) t += dslots[w];
 		*mean_loss = (float) (t / (double) n_rows);
-		g_xent_arrivals = 0u;
 	}
 }
 
@@ -145,7 +135,8 @@ __device__ __forceinline__ void smx_regs(int n_rows, int n_cols, const T * X, TO
 					const float d = rnd_in<T>(diff);
 					const float ex = exp_fast(d);
 					if (e & 1) sd1 += ex; else sd0 += ex;
-					if (FUSED) corr = fmaf(ex, diff - d, corr);
+					/* fmaxf drops the NaN of -inf - (-inf) (where ex is 0 anyway) */
+					if (FUSED) corr = fmaf(ex, fmaxf(diff - d, -1.0f), corr);
 					f[e] = d;
 				}
 				xr[c] = pack16<T>(f);   /* d is exact in T */
@@ -224,12 +215,10 @@ __device__ __forceinline__ void smx_stream(int n_rows, int n_cols, const T * X, 
 template <typename T, typename TO, bool FUSED>
 __device__ __forceinline__ void smx(int n_rows, int n_cols, const T * X, TO * out, const uint32_t * labels, float * loss, float * mean_loss) {
 	constexpr int VEC = VecOf<T>::N;
-	__shared__ double dslots[16];
 	const bool vec_ok = (n_cols % VEC == 0) && aligned16(X) && aligned16(out)
 						&& ((n_cols / VEC + (int) blockDim.x - 1) / (int) blockDim.x) <= SMX_MAXCH;
 	if (vec_ok) smx_regs<T, TO, FUSED>(n_rows, n_cols, X, out, labels, loss);
 	else smx_stream<T, TO, FUSED>(n_rows, n_cols, X, out, labels, loss);
-	if (FUSED && mean_loss && loss) finish_mean_loss(n_rows, loss, mean_loss, dslots);
 }
 
 #define SMX_KERNELS(SUFFIX, PSUFFIX, T)                                                                                \
@@ -240,6 +229,10 @@ __device__ __forceinline__ void smx(int n_rows, int n_cols, const T * X, TO * ou
 	extern "C" __global__ void __launch_bounds__(SMX_THREADS) softmax_cross_entropy_loss_##SUFFIX##_kernel(int n_rows, \
 			int n_cols, T * logits, uint32_t * labels, float * loss, float * mean_loss) {                              \
 		smx<T, T, true>(n_rows, n_cols, logits, logits, labels, loss, mean_loss);                                      \
+	}                                                                                                                  \
+	extern "C" __global__ void __launch_bounds__(SMX_THREADS) softmax_cross_entropy_loss_##SUFFIX##_kernel_finish(      \
+			int n_rows, int n_cols, T * logits, uint32_t * labels, float * loss, float * mean_loss) {                  \
+		mean_loss_finish(n_rows, loss, mean_loss);                                                                     \
 	}                                                                                                                  \
 	extern "C" __global__ void __launch_bounds__(256) cross_entropy_loss_##SUFFIX##_kernel(int n_rows, int n_cols,     \
 			T * pred_logits, uint32_t * labels) {                                                                      \

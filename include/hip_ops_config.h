@@ -36,6 +36,7 @@ int softmax_set_launch_config(Hip_Launch_Config * hip_launch_config, Dataflow_Ha
 int cross_entropy_loss_set_launch_config(Hip_Launch_Config * hip_launch_config, Dataflow_Handle * dataflow_handle, Hip_Function * hip_function, Op * op);
 /* fused softmax + cross-entropy (no reference counterpart) */
 int softmax_cross_entropy_loss_set_launch_config(Hip_Launch_Config * hip_launch_config, Dataflow_Handle * dataflow_handle, Hip_Function * hip_function, Op * op);
+int softmax_cross_entropy_loss_set_finish_launch_config(Hip_Launch_Config * hip_launch_config, Dataflow_Handle * dataflow_handle, Hip_Function * hip_function, Op * op);
 
 #ifdef __cplusplus
 }
