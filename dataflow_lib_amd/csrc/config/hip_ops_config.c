@@ -205,7 +205,7 @@ int swiglu_bwd_x_set_launch_config(Hip_Launch_Config * hip_launch_config, Datafl
 /* ---------------- softmax / cross-entropy ---------------- */
 
 /* one workgroup per row; small rows get a smaller workgroup */
-static int smx_config(Hip_Launch_Config * c, Hip_Function * f, int n_rows, int n_cols, const char * what) {
+static int smx_config(Hip_Launch_Config * c, Dataflow_Handle * h, Hip_Function * f, int n_rows, int n_cols, const char * what) {
 	const size_t elem = arg_elem_bytes(f, 2);
 	if (n_rows < 0 || n_cols < 0 || elem == 0) {
 		fprintf(stderr, "Error: %s: invalid shape (%d x %d) or dtype...\n", what, n_rows, n_cols);
@@ -215,25 +215,23 @@ static int smx_config(Hip_Launch_Config * c, Hip_Function * f, int n_rows, int n
 		set_1d(c, 0, 1, 0);
 		return 0;
 	}
-	const long nv = MY_CEIL((long) n_cols, (long) (16 / elem));
-	long block = MY_CEIL(MY_CEIL(nv, (long) SMX_MAXCH), 64L) * 64L;
-	block = MY_MAX(64L, MY_MIN(block, (long) SMX_THREADS));
-	set_1d(c, (unsigned) n_rows, (unsigned) block, 0);
+	/* persistent over rows: one workgroup of SMX_THREADS per CU (a row fills
+	 * its VGPRs and half its LDS) */
+	const long grid = MY_MIN((long) n_rows, (long) dev(h)->cu_count);
+	set_1d(c, (unsigned) grid, SMX_THREADS, 0);
 	return 0;
 }
 
 int softmax_set_launch_config(Hip_Launch_Config * hip_launch_config, Dataflow_Handle * dataflow_handle, Hip_Function * hip_function, Op * op) {
-	(void) dataflow_handle;
-	return smx_config(hip_launch_config, hip_function, ARG(op, 0, int), ARG(op, 1, int), "softmax");
+	return smx_config(hip_launch_config, dataflow_handle, hip_function, ARG(op, 0, int), ARG(op, 1, int), "softmax");
 }
 
 int softmax_cross_entropy_loss_set_launch_config(Hip_Launch_Config * hip_launch_config, Dataflow_Handle * dataflow_handle, Hip_Function * hip_function, Op * op) {
-	(void) dataflow_handle;
 	if (ARG(op, 5, float *) && !ARG(op, 4, float *)) {
 		fprintf(stderr, "Error: softmax cross entropy loss: mean_loss needs the per-row loss buffer...\n");
 		return -1;
 	}
-	return smx_config(hip_launch_config, hip_function, ARG(op, 0, int), ARG(op, 1, int), "softmax cross entropy loss");
+	return smx_config(hip_launch_config, dataflow_handle, hip_function, ARG(op, 0, int), ARG(op, 1, int), "softmax cross entropy loss");
 }
 
 int softmax_cross_entropy_loss_set_finish_launch_config(Hip_Launch_Config * hip_launch_config, Dataflow_Handle * dataflow_handle, Hip_Function * hip_function, Op * op) {

@@ -111,6 +111,13 @@ template <typename T> struct Chunk<T, 1> {
 
 __device__ __forceinline__ bool aligned16(const void * p) { return (((uintptr_t) p) & 15u) == 0; }
 
+/* Empty register barrier: tells the compiler the 16 bytes may have changed,
+ * so values derived from them earlier (unpacked floats) are recomputed from
+ * the packed registers instead of being kept alive (and spilled) across a pass. */
+__device__ __forceinline__ void reg_barrier(R16 & r) {
+	__asm__ volatile("" : "+v"(r.w[0]), "+v"(r.w[1]), "+v"(r.w[2]), "+v"(r.w[3]));
+}
+
 /* 16-byte global accesses with the non-temporal hint, for data each kernel
  * touches exactly once */
 __device__ __forceinline__ R16 ld16_nt(const void * p) {

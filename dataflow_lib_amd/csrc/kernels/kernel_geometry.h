@@ -27,6 +27,8 @@
  * SMX_THREADS * SMX_MAXCH 16-byte chunks held in registers */
 #define SMX_THREADS 1024
 #define SMX_MAXCH 16
+/* chunks per thread of the next row prefetched into LDS (8 x 16 KB) */
+#define SMX_PF 8
 
 /* RoPE: one wave per token, 4 waves per workgroup, head_dim <= 512 */
 #define ROPE_MAX_HEAD_DIM 512

@@ -76,23 +76,47 @@ __device__ __forceinline__ void mean_loss_finish(int n_rows, const float * loss,
 	}
 }
 
-/* register-resident row path: rows of at most SMX_MAXCH 16-byte chunks per
- * thread; chunk c of thread t is row chunk c * blockDim.x + t, addressed
- * through a per-row buffer resource (one VGPR offset for all chunks) */
+/* waits for every outstanding vector-memory access of this wave
+ * (s_waitcnt vmcnt(0); expcnt and lgkmcnt left at their maxima) */
+#define WAIT_VMEM_ALL() __builtin_amdgcn_s_waitcnt(0x0F70)
+/* waits for every outstanding LDS access of this wave (lgkmcnt(0)) */
+#define WAIT_LDS_ALL() __builtin_amdgcn_s_waitcnt(0xC07F)
+
+typedef __attribute__((address_space(3))) void * lds_ptr_t;
+
+/* Register-resident row path, persistent over rows (row = block, block +
+ * grid, ...). Chunk c of thread t is row chunk c * blockDim + t, addressed
+ * through a per-row buffer resource (one VGPR offset for all chunks); the
+ * whole row sits in VGPRs. The first SMX_PF chunks of the NEXT row are
+ * prefetched straight into LDS (16-byte buffer loads with the LDS bit) while
+ * the current row computes, so half of each row's HBM read overlaps the
+ * arithmetic of the previous row; the other half is loaded into VGPRs at the
+ * top of its row, behind the previous row's stores. Each wave prefetches into and reads from
+ * its own LDS slice only, so no workgroup barrier guards the buffer. */
 template <typename T, typename TO, bool FUSED>
 __device__ __forceinline__ void smx_regs(int n_rows, int n_cols, const T * X, TO * out, const uint32_t * labels, float * loss) {
 	constexpr int VEC = VecOf<T>::N;
 	static_assert(sizeof(T) == sizeof(TO), "in-register output packing needs equal widths");
 	__shared__ float slots[32];
+	__shared__ __attribute__((aligned(16))) R16 pf[SMX_PF * SMX_THREADS];
 	const int tid = threadIdx.x;
-	const int nt = blockDim.x;
+	constexpr int nt = SMX_THREADS;          /* the launch guarantees blockDim.x == SMX_THREADS */
+	constexpr uint32_t cstride = nt * 16u;   /* chunk stride: an immediate, rematerialised per use */
+	const int wave_base = tid & ~63;
 	const int nv = n_cols / VEC;
 	const int nch = (nv + nt - 1) / nt;
 	const uint32_t row_bytes = (uint32_t) n_cols * (uint32_t) sizeof(T);
 	const uint32_t voff = (uint32_t) tid * 16u;
-	const uint32_t cstride = (uint32_t) nt * 16u;
 
-	for (int row = blockIdx.x; row < n_rows; row += gridDim.x) {
+	int row = blockIdx.x;
+	/* prologue: the LDS part of this workgroup's first row */
+	if (row < n_rows) {
+		const __amdgpu_buffer_rsrc_t r0 = make_rsrc(X + (long) row * n_cols, row_bytes);
+#pragma unroll
+		for (int c = 0; c < SMX_PF; c++)
+			if (c < nch) __builtin_amdgcn_raw_ptr_buffer_load_lds(r0, (lds_ptr_t) &pf[c * nt + wave_base], 16, voff, c * cstride, 0, BUF_AUX_NT);
+	}
+	for (; row < n_rows; row += gridDim.x) {
 		const __amdgpu_buffer_rsrc_t rin = make_rsrc(X + (long) row * n_cols, row_bytes);
 		const __amdgpu_buffer_rsrc_t rout = make_rsrc(out + (long) row * n_cols, row_bytes);
 		uint32_t lab = 0xffffffffu;
@@ -101,13 +125,30 @@ __device__ __forceinline__ void smx_regs(int n_rows, int n_cols, const T * X, TO
 			lab = labels[row];
 			if (tid == 0 && lab < (uint32_t) n_cols) x_lab = to_f(X[(long) row * n_cols + lab]);
 		}
-
+		/* the register part of this row, then the prefetched part from the
+		 * wave's own LDS slice */
 		R16 xr[SMX_MAXCH];
+#pragma unroll
+		for (int c = SMX_PF; c < SMX_MAXCH; c++)
+			if (c < nch) xr[c] = buf_load16_nt(rin, voff, c * cstride);
+		WAIT_VMEM_ALL();
+#pragma unroll
+		for (int c = 0; c < SMX_PF; c++)
+			if (c < nch) xr[c] = pf[c * nt + tid];
+		WAIT_LDS_ALL();
+		/* start the next row's LDS part now; it lands while this row computes */
+		const int next = row + gridDim.x;
+		if (next < n_rows) {
+			const __amdgpu_buffer_rsrc_t rn = make_rsrc(X + (long) next * n_cols, row_bytes);
+#pragma unroll
+			for (int c = 0; c < SMX_PF; c++)
+				if (c < nch) __builtin_amdgcn_raw_ptr_buffer_load_lds(rn, (lds_ptr_t) &pf[c * nt + wave_base], 16, voff, c * cstride, 0, BUF_AUX_NT);
+		}
+
 		float m = -__builtin_inff();
 #pragma unroll
 		for (int c = 0; c < SMX_MAXCH; c++) {
 			if (c < nch) {
-				xr[c] = buf_load16_nt(rin, voff, c * cstride);
 				float f[VEC];
 				unpack16<T>(xr[c], f);
 				float cm = f[0];
@@ -118,6 +159,8 @@ __device__ __forceinline__ void smx_regs(int n_rows, int n_cols, const T * X, TO
 			}
 		}
 		m = block_max(m, slots);
+#pragma unroll
+		for (int c = 0; c < SMX_MAXCH; c++) reg_barrier(xr[c]);
 
 		/* sd = sum exp(d) with d = rnd(x - m); the fused op also needs
 		 * sx = sum exp(x - m) = sum exp(d) * exp(delta), delta = (x - m) - d
@@ -146,7 +189,8 @@ __device__ __forceinline__ void smx_regs(int n_rows, int n_cols, const T * X, TO
 		float sx = sd + corr;
 		__syncthreads();   /* slots reuse */
 		block_sum2(sd, sx, slots);
-		const float inv = 1.0f / sd;
+		/* y = exp(d) / sd as one exp2: exp2(d * log2(e) - log2(sd)) */
+		const float nlog2s = -__builtin_amdgcn_logf(sd);
 
 		/* chunk and lane holding the label (if any) */
 		const int lab_chunk = (lab < (uint32_t) n_cols) ? (int) (lab / VEC) : -1;
@@ -156,7 +200,7 @@ __device__ __forceinline__ void smx_regs(int n_rows, int n_cols, const T * X, TO
 				float f[VEC];
 				unpack16<T>(xr[c], f);
 #pragma unroll
-				for (int e = 0; e < VEC; e++) f[e] = exp_fast(f[e]) * inv;
+				for (int e = 0; e < VEC; e++) f[e] = __builtin_amdgcn_exp2f(fmaf(f[e], SMX_LOG2E, nlog2s));
 				if (FUSED && (c * nt + tid) == lab_chunk) {
 					const int le = (int) (lab % VEC);
 #pragma unroll
@@ -171,6 +215,7 @@ __device__ __forceinline__ void smx_regs(int n_rows, int n_cols, const T * X, TO
 		}
 		__syncthreads();   /* slots reuse by the next row */
 	}
+	WAIT_VMEM_ALL();
 }
 
 /* any row length / alignment: three passes over global memory per row */
@@ -215,8 +260,8 @@ __device__ __forceinline__ void smx_stream(int n_rows, int n_cols, const T * X, 
 template <typename T, typename TO, bool FUSED>
 __device__ __forceinline__ void smx(int n_rows, int n_cols, const T * X, TO * out, const uint32_t * labels, float * loss, float * mean_loss) {
 	constexpr int VEC = VecOf<T>::N;
-	const bool vec_ok = (n_cols % VEC == 0) && aligned16(X) && aligned16(out)
-						&& ((n_cols / VEC + (int) blockDim.x - 1) / (int) blockDim.x) <= SMX_MAXCH;
+	const bool vec_ok = (n_cols % VEC == 0) && aligned16(X) && aligned16(out) && blockDim.x == SMX_THREADS
+						&& ((n_cols / VEC + SMX_THREADS - 1) / SMX_THREADS) <= SMX_MAXCH;
 	if (vec_ok) smx_regs<T, TO, FUSED>(n_rows, n_cols, X, out, labels, loss);
 	else smx_stream<T, TO, FUSED>(n_rows, n_cols, X, out, labels, loss);
 }
