@@ -52,13 +52,33 @@ static int rms_check(const char * what, int n_rows, int n_cols, size_t elem) {
 	return 0;
 }
 
-/* rows per workgroup-iteration and grid for the row-streaming ops */
-static void rms_rowwise(Hip_Launch_Config * c, Dataflow_Handle * h, int n_rows, int nv) {
+/* workgroups of this function that are resident on the whole device at once */
+static long resident_groups(Dataflow_Handle * h, Hip_Function * f, int block, size_t lds) {
+	int per_cu = 0;
+	if (hipModuleOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, f->function_handle, block, lds) != hipSuccess || per_cu < 1) per_cu = 1;
+	return (long) per_cu * (long) dev(h)->cu_count;
+}
+
+/* Row slots per CU for the row-streaming RMSNorm ops: each slot keeps two rows
+ * of `arrays` input rows in flight (the current one and the prefetched next
+ * one), and about RMS_INFLIGHT_BYTES outstanding per CU measured best: more
+ * concurrent row streams only add DRAM page misses. */
+static long rms_slots_per_cu(int n_cols, size_t elem, int arrays) {
+	const long per_slot = 2L * (long) n_cols * (long) elem * (long) arrays;
+	long s = per_slot > 0 ? (long) RMS_INFLIGHT_BYTES / per_slot : 1;
+	return MY_MAX(1L, MY_MIN(s, 32L));
+}
+
+/* fwd / bwd_x: ~256-thread workgroups, as many per CU as the slot target asks */
+static void rms_rowwise(Hip_Launch_Config * c, Dataflow_Handle * h, Hip_Function * f, int n_rows, int n_cols, size_t elem, int nv, int arrays) {
 	const int tpr = rms_tpr_for(nv);
-	/* two row slots per workgroup up to 512 threads, four workgroups per CU */
-	const int slots = MY_MAX(1, 512 / tpr);
-	long grid = MY_MIN((long) MY_CEIL(n_rows, slots), (long) dev(h)->cu_count * 4L);
-	set_1d(c, (unsigned) grid, (unsigned) (slots * tpr), (unsigned) (RMS_CELLS_PER_SLOT * slots * sizeof(float)));
+	const int slots = MY_MAX(1, 256 / tpr);
+	const unsigned block = (unsigned) (slots * tpr);
+	const unsigned lds = (unsigned) (RMS_CELLS_PER_SLOT * slots * sizeof(float));
+	const long groups_per_cu = MY_CEIL(rms_slots_per_cu(n_cols, elem, arrays), (long) slots);
+	long grid = MY_MIN((long) MY_CEIL(n_rows, slots), (long) dev(h)->cu_count * groups_per_cu);
+	grid = MY_MIN(grid, resident_groups(h, f, (int) block, lds));
+	set_1d(c, (unsigned) grid, block, lds);
 }
 
 int rms_norm_set_launch_config(Hip_Launch_Config * hip_launch_config, Dataflow_Handle * dataflow_handle, Hip_Function * hip_function, Op * op) {
@@ -66,7 +86,7 @@ int rms_norm_set_launch_config(Hip_Launch_Config * hip_launch_config, Dataflow_H
 	const size_t elem = arg_elem_bytes(hip_function, 3);
 	if (rms_check("rms norm", n_rows, n_cols, elem)) return -1;
 	const int nv = rms_vec_chunks(n_cols, (int) elem, ptr_bits(ARG(op, 3, void *)) | ptr_bits(ARG(op, 4, void *)) | ptr_bits(ARG(op, 5, void *)));
-	rms_rowwise(hip_launch_config, dataflow_handle, (n_cols == 0) ? 0 : n_rows, nv);
+	rms_rowwise(hip_launch_config, dataflow_handle, hip_function, (n_cols == 0) ? 0 : n_rows, n_cols, elem, nv, 1);
 	return 0;
 }
 
@@ -76,19 +96,21 @@ int rms_norm_bwd_x_set_launch_config(Hip_Launch_Config * hip_launch_config, Data
 	if (rms_check("rms norm bwd x", n_rows, n_cols, elem)) return -1;
 	const int nv = rms_vec_chunks(n_cols, (int) elem, ptr_bits(ARG(op, 5, void *)) | ptr_bits(ARG(op, 6, void *)) |
 													ptr_bits(ARG(op, 7, void *)) | ptr_bits(ARG(op, 8, void *)));
-	rms_rowwise(hip_launch_config, dataflow_handle, (n_cols == 0) ? 0 : n_rows, nv);
+	rms_rowwise(hip_launch_config, dataflow_handle, hip_function, (n_cols == 0) ? 0 : n_rows, n_cols, elem, nv, 3);
 	return 0;
 }
 
 /* two-pass dW ops: pick slots and grid so LDS and the partial scratch fit */
-static int rms_dw_config(Hip_Launch_Config * c, Dataflow_Handle * h, Hip_Function * f, const char * what, int n_rows, int n_cols, int nv) {
+static int rms_dw_config(Hip_Launch_Config * c, Dataflow_Handle * h, Hip_Function * f, const char * what, int n_rows, int n_cols, size_t elem, int nv, int arrays) {
 	if (n_rows == 0 || n_cols == 0) {
 		set_1d(c, 0, 1, 0);
 		return 0;
 	}
 	const int tpr = rms_tpr_for(nv);
 	const long max_lds = f->function_config.func_max_smem > 0 ? f->function_config.func_max_smem : dev(h)->max_smem_per_block;
-	int slots = MY_MAX(1, RMS_MAX_TPR / tpr);
+	/* one workgroup per CU holding the CU's row slots (one dW partial row per
+	 * workgroup) */
+	int slots = (int) MY_MIN(rms_slots_per_cu(n_cols, elem, arrays), (long) MY_MAX(1, RMS_MAX_TPR / tpr));
 	long lds = 0;
 	for (; slots >= 1; slots--) {
 		const long colbuf = (nv > 0) ? (long) n_cols : (long) slots * n_cols;
@@ -124,7 +146,7 @@ int rms_norm_bwd_w_set_launch_config(Hip_Launch_Config * hip_launch_config, Data
 	const size_t elem = arg_elem_bytes(hip_function, 4);
 	if (rms_check("rms norm bwd w", n_rows, n_cols, elem)) return -1;
 	const int nv = rms_vec_chunks(n_cols, (int) elem, ptr_bits(ARG(op, 4, void *)) | ptr_bits(ARG(op, 5, void *)));
-	return rms_dw_config(hip_launch_config, dataflow_handle, hip_function, "rms norm bwd w", n_rows, n_cols, nv);
+	return rms_dw_config(hip_launch_config, dataflow_handle, hip_function, "rms norm bwd w", n_rows, n_cols, elem, nv, 2);
 }
 
 int rms_norm_bwd_w_set_finish_launch_config(Hip_Launch_Config * hip_launch_config, Dataflow_Handle * dataflow_handle, Hip_Function * hip_function, Op * op) {
@@ -139,7 +161,7 @@ int rms_norm_bwd_set_launch_config(Hip_Launch_Config * hip_launch_config, Datafl
 	if (rms_check("rms norm bwd", n_rows, n_cols, elem)) return -1;
 	const int nv = rms_vec_chunks(n_cols, (int) elem, ptr_bits(ARG(op, 4, void *)) | ptr_bits(ARG(op, 5, void *)) |
 													ptr_bits(ARG(op, 6, void *)) | ptr_bits(ARG(op, 7, void *)));
-	return rms_dw_config(hip_launch_config, dataflow_handle, hip_function, "rms norm bwd", n_rows, n_cols, nv);
+	return rms_dw_config(hip_launch_config, dataflow_handle, hip_function, "rms norm bwd", n_rows, n_cols, elem, nv, 3);
 }
 
 int rms_norm_bwd_set_finish_launch_config(Hip_Launch_Config * hip_launch_config, Dataflow_Handle * dataflow_handle, Hip_Function * hip_function, Op * op) {
@@ -161,6 +183,7 @@ static int rope_config(Hip_Launch_Config * c, Dataflow_Handle * h, Op * op, cons
 		return -1;
 	}
 	const uint64_t n_tokens = N / (uint64_t) model_dim;
+	/* one wave per token, looping; four workgroups per CU measured best */
 	uint64_t grid = MY_CEIL(n_tokens, (uint64_t) ROPE_WAVES);
 	grid = MY_MIN(grid, (uint64_t) dev(h)->cu_count * 4u);
 	set_1d(c, (unsigned) grid, 64 * ROPE_WAVES, 0);

@@ -18,6 +18,9 @@
 #define RMS_STREAM_TPR 256
 /* LDS floats per row slot for the row reductions: [2 parities][32] */
 #define RMS_CELLS_PER_SLOT 64
+/* launch target: bytes of row loads outstanding per CU (each row slot keeps
+ * its current and next row in flight) */
+#define RMS_INFLIGHT_BYTES (64 * 1024)
 /* dW finish kernel: 64 columns per workgroup, partial rows spread over its waves */
 #define RMS_FINISH_THREADS 1024
 /* fp32 partial rows for the two-pass dW reduction (16 MiB) */

@@ -78,6 +78,48 @@ __device__ __forceinline__ void write_partial_from_lds(const float * colbuf, int
 	for (int j = threadIdx.x; j < n_cols; j += blockDim.x) part[j] = colbuf[j];
 }
 
+/* One row of a row-major tensor as a buffer range. A row past the end gets an
+ * empty range: its loads return zero and its stores are dropped. `row` must be
+ * wave-uniform (it lives in SGPRs). */
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t row_rsrc(const void * base, int row, int n_rows, uint32_t row_bytes) {
+	const bool live = row < n_rows;
+	return make_rsrc(static_cast<const char *>(base) + (long) (live ? row : 0) * row_bytes, live ? row_bytes : 0u);
+}
+
+/* the registers one row slot holds for one row */
+template <int MODE>
+struct RmsRow {
+	R16 x[RMS_CH], g[RMS_CH], d[RMS_CH];
+	float r, ws;
+};
+
+/* Issue the loads of `row` (wave-uniform). Chunks a thread does not own lie
+ * past the row's byte range, so they read as zero. */
+template <typename T, int MODE>
+__device__ __forceinline__ void rms_load_row(const RmsArgs & a, int row, uint32_t row_bytes, const uint32_t * voff, RmsRow<MODE> & o) {
+	const __amdgpu_buffer_rsrc_t rx = row_rsrc(a.X, row, a.n_rows, row_bytes);
+#pragma unroll
+	for (int c = 0; c < RMS_CH; c++) o.x[c] = buf_load16_nt(rx, voff[c], 0);
+	if (MODE != RMS_FWD) {
+		const __amdgpu_buffer_rsrc_t rg = row_rsrc(a.dY, row, a.n_rows, row_bytes);
+#pragma unroll
+		for (int c = 0; c < RMS_CH; c++) o.g[c] = buf_load16_nt(rg, voff[c], 0);
+	}
+	if (MODE == RMS_BWD_X || MODE == RMS_BWD) {
+		const __amdgpu_buffer_rsrc_t rd = row_rsrc(a.Y_or_dX, row, a.n_rows, row_bytes);
+#pragma unroll
+		for (int c = 0; c < RMS_CH; c++) o.d[c] = buf_load16_nt(rd, voff[c], 0);
+	}
+	const bool live = row < a.n_rows;
+	o.r = (MODE != RMS_FWD && live) ? a.rs_in[row] : 0.0f;
+	o.ws = (MODE == RMS_BWD_X && live) ? a.ws_in[row] : 0.0f;
+}
+
+/*
+ * Vector path, software-pipelined: while a slot reduces and writes row i it
+ * already has the loads of its next row (i + grid * slots) in flight, so the
+ * memory pipe does not drain at the row reduction's barrier.
+ */
 template <typename T, typename TW, int MODE>
 __device__ __forceinline__ void rms_vector(const RmsArgs & a, int nv, float * lds) {
 	constexpr int V = VecOf<T>::N;
@@ -88,15 +130,18 @@ __device__ __forceinline__ void rms_vector(const RmsArgs & a, int nv, float * ld
 	const int wps = tpr >> 6;
 	const int wis = tr >> 6;
 	const int n_cols = a.n_cols;
-	const R16 * W = reinterpret_cast<const R16 *>(a.W);
+	const uint32_t row_bytes = (uint32_t) n_cols * (uint32_t) sizeof(T);
 
+	uint32_t voff[RMS_CH];
 	bool own[RMS_CH];
 	R16 wr[RMS_CH];
 	float acc[RMS_CH][V];
+	const __amdgpu_buffer_rsrc_t rw = make_rsrc(a.W, (MODE != RMS_BWD_W) ? row_bytes : 0u);
 #pragma unroll
 	for (int c = 0; c < RMS_CH; c++) {
+		voff[c] = (uint32_t) (c * tpr + tr) * 16u;
 		own[c] = (c * tpr + tr) < nv;
-		if (MODE != RMS_BWD_W) wr[c] = own[c] ? W[c * tpr + tr] : Chunk<T, V>::zero();
+		wr[c] = buf_load16(rw, voff[c], 0);
 #pragma unroll
 		for (int e = 0; e < V; e++) acc[c][e] = 0.0f;
 	}
@@ -104,82 +149,72 @@ __device__ __forceinline__ void rms_vector(const RmsArgs & a, int nv, float * ld
 	float * cells = lds;                                   /* [2][slots][32] */
 	float * colbuf = lds + RMS_CELLS_PER_SLOT * slots;     /* [n_cols] for the dW modes */
 	int parity = 0;
+	const int step = gridDim.x * slots;
+	/* tpr is a multiple of 64, so the row is uniform over each wave */
+	int row = __builtin_amdgcn_readfirstlane(blockIdx.x * slots + slot);
+	RmsRow<MODE> cur;
+	rms_load_row<T, MODE>(a, row, row_bytes, voff, cur);
 
-	for (int base_row = blockIdx.x * slots; base_row < a.n_rows; base_row += gridDim.x * slots) {
-		const int row = base_row + slot;
+	for (int base_row = blockIdx.x * slots; base_row < a.n_rows; base_row += step) {
+		const int nrow = row + step;
+		RmsRow<MODE> nxt;
+		rms_load_row<T, MODE>(a, nrow, row_bytes, voff, nxt);
 		const bool live = row < a.n_rows;
-		const long off = (long) row * (n_cols / V);
-		const R16 * xrow = reinterpret_cast<const R16 *>(a.X) + off;
-		R16 xr[RMS_CH], gr[RMS_CH];
-#pragma unroll
-		for (int c = 0; c < RMS_CH; c++) {
-			const bool ok = live && own[c];
-			xr[c] = ok ? xrow[c * tpr + tr] : Chunk<T, V>::zero();
-			if (MODE != RMS_FWD) gr[c] = ok ? (reinterpret_cast<const R16 *>(a.dY) + off)[c * tpr + tr] : Chunk<T, V>::zero();
-		}
+		const __amdgpu_buffer_rsrc_t ro = row_rsrc(a.Y_or_dX, row, a.n_rows, row_bytes);
 
 		if (MODE == RMS_FWD) {
 			float ss = 0.0f, sw = 0.0f;
 #pragma unroll
 			for (int c = 0; c < RMS_CH; c++) {
 				float xf[V], wf[V];
-				unpack16<T>(xr[c], xf);
+				unpack16<T>(cur.x[c], xf);
 				unpack16<T>(wr[c], wf);
 #pragma unroll
 				for (int e = 0; e < V; e++) { sw = fmaf(xf[e], wf[e], sw); ss = fmaf(xf[e], xf[e], ss); }
 			}
 			slot_sum2(ss, sw, cells, parity, slot, wis, wps, slots);
 			parity ^= 1;
-			if (live) {
-				const float r = 1.0f / sqrtf(ss / (float) n_cols + a.eps);
-				if (tr == 0) {
-					if (a.ws_out) a.ws_out[row] = sw;
-					if (a.rs_out) a.rs_out[row] = r;
-				}
-				R16 * yrow = reinterpret_cast<R16 *>(a.Y_or_dX) + off;
 #pragma unroll
-				for (int c = 0; c < RMS_CH; c++) {
-					if (own[c]) {
-						float xf[V], wf[V];
-						unpack16<T>(xr[c], xf);
-						unpack16<T>(wr[c], wf);
+			for (int c = 0; c < RMS_CH; c++) { reg_barrier(cur.x[c]); reg_barrier(wr[c]); }
+			const float r = 1.0f / sqrtf(ss / (float) n_cols + a.eps);
+			if (live && tr == 0) {
+				if (a.ws_out) a.ws_out[row] = sw;
+				if (a.rs_out) a.rs_out[row] = r;
+			}
 #pragma unroll
-						for (int e = 0; e < V; e++) xf[e] = (xf[e] * r) * wf[e];
-						yrow[c * tpr + tr] = pack16<T>(xf);
-					}
-				}
+			for (int c = 0; c < RMS_CH; c++) {
+				float xf[V], wf[V];
+				unpack16<T>(cur.x[c], xf);
+				unpack16<T>(wr[c], wf);
+#pragma unroll
+				for (int e = 0; e < V; e++) xf[e] = (xf[e] * r) * wf[e];
+				buf_store16_nt(ro, voff[c], 0, pack16<T>(xf));
 			}
 		}
 		else if (MODE == RMS_BWD_X) {
-			if (live) {
-				const float r = a.rs_in[row];
-				const float ws = a.ws_in[row];
-				const float r3 = r * r * r;
-				R16 * drow = reinterpret_cast<R16 *>(a.Y_or_dX) + off;
+			const float r = cur.r;
+			const float r3 = r * r * r;
 #pragma unroll
-				for (int c = 0; c < RMS_CH; c++) {
-					if (own[c]) {
-						float wf[V], xf[V], gf[V], df[V];
-						unpack16<T>(wr[c], wf);
-						unpack16<T>(xr[c], xf);
-						unpack16<T>(gr[c], gf);
-						unpack16<T>(drow[c * tpr + tr], df);
+			for (int c = 0; c < RMS_CH; c++) {
+				float wf[V], xf[V], gf[V], df[V];
+				unpack16<T>(wr[c], wf);
+				unpack16<T>(cur.x[c], xf);
+				unpack16<T>(cur.g[c], gf);
+				unpack16<T>(cur.d[c], df);
 #pragma unroll
-						for (int e = 0; e < V; e++) df[e] = bwd_x_elem<T>(wf[e], xf[e], gf[e], df[e], r, r3, ws, n_cols);
-						drow[c * tpr + tr] = pack16<T>(df);
-					}
-				}
+				for (int e = 0; e < V; e++) df[e] = bwd_x_elem<T>(wf[e], xf[e], gf[e], df[e], r, r3, cur.ws, n_cols);
+				buf_store16_nt(ro, voff[c], 0, pack16<T>(df));
 			}
 		}
 		else {
-			const float r = live ? a.rs_in[row] : 0.0f;
+			const float r = cur.r;
 			if (MODE == RMS_BWD) {
 				float dot = 0.0f;
 #pragma unroll
 				for (int c = 0; c < RMS_CH; c++) {
 					float xf[V], gf[V], wf[V];
-					unpack16<T>(xr[c], xf);
-					unpack16<T>(gr[c], gf);
+					unpack16<T>(cur.x[c], xf);
+					unpack16<T>(cur.g[c], gf);
 					unpack16<T>(wr[c], wf);
 #pragma unroll
 					for (int e = 0; e < V; e++) dot = fmaf(gf[e] * wf[e], xf[e], dot);
@@ -187,34 +222,34 @@ __device__ __forceinline__ void rms_vector(const RmsArgs & a, int nv, float * ld
 				float unused = 0.0f;
 				slot_sum2(dot, unused, cells, parity, slot, wis, wps, slots);
 				parity ^= 1;
-				if (live) {
-					const float coef = ((r * r * r) * dot) / (float) n_cols;
-					R16 * drow = reinterpret_cast<R16 *>(a.Y_or_dX) + off;
+				/* re-unpack after the barrier instead of holding the floats across it */
 #pragma unroll
-					for (int c = 0; c < RMS_CH; c++) {
-						if (own[c]) {
-							float xf[V], gf[V], wf[V], df[V];
-							unpack16<T>(xr[c], xf);
-							unpack16<T>(gr[c], gf);
-							unpack16<T>(wr[c], wf);
-							unpack16<T>(drow[c * tpr + tr], df);
+				for (int c = 0; c < RMS_CH; c++) { reg_barrier(cur.x[c]); reg_barrier(cur.g[c]); reg_barrier(wr[c]); }
+				const float coef = ((r * r * r) * dot) / (float) n_cols;
 #pragma unroll
-							for (int e = 0; e < V; e++) df[e] = df[e] + (r * (gf[e] * wf[e]) - xf[e] * coef);
-							drow[c * tpr + tr] = pack16<T>(df);
-						}
-					}
+				for (int c = 0; c < RMS_CH; c++) {
+					float xf[V], gf[V], wf[V], df[V];
+					unpack16<T>(cur.x[c], xf);
+					unpack16<T>(cur.g[c], gf);
+					unpack16<T>(wr[c], wf);
+					unpack16<T>(cur.d[c], df);
+#pragma unroll
+					for (int e = 0; e < V; e++) df[e] = df[e] + (r * (gf[e] * wf[e]) - xf[e] * coef);
+					buf_store16_nt(ro, voff[c], 0, pack16<T>(df));
 				}
 			}
-			/* dead rows load zeros, so they add nothing */
+			/* rows past the end loaded zeros and r = 0, so they add nothing */
 #pragma unroll
 			for (int c = 0; c < RMS_CH; c++) {
 				float xf[V], gf[V];
-				unpack16<T>(xr[c], xf);
-				unpack16<T>(gr[c], gf);
+				unpack16<T>(cur.x[c], xf);
+				unpack16<T>(cur.g[c], gf);
 #pragma unroll
 				for (int e = 0; e < V; e++) acc[c][e] = fmaf(gf[e] * xf[e], r, acc[c][e]);
 			}
 		}
+		cur = nxt;
+		row = nrow;
 	}
 
 	if (MODE == RMS_BWD_W || MODE == RMS_BWD) {
