@@ -149,9 +149,18 @@ __device__ __forceinline__ R16 buf_load16(__amdgpu_buffer_rsrc_t r, uint32_t vof
 	o.w[0] = v.x; o.w[1] = v.y; o.w[2] = v.z; o.w[3] = v.w;
 	return o;
 }
+/* A VALU write to a data VGPR of a wider-than-8-byte buffer store issued just
+ * before it can change the data the store writes (observed on gfx950 with an
+ * SGPR soffset, where the compiler inserts no wait). So every 16-byte buffer
+ * store is followed by two wait states during which its data registers stay
+ * unchanged (they are inputs of the s_nop). */
+__device__ __forceinline__ void store_data_guard(const u32x4_v & v) {
+	__asm__ volatile("s_nop 1" : : "v"(v) : "memory");
+}
 __device__ __forceinline__ void buf_store16(__amdgpu_buffer_rsrc_t r, uint32_t voff, uint32_t soff, const R16 & x) {
 	const u32x4_v v = {x.w[0], x.w[1], x.w[2], x.w[3]};
 	__builtin_amdgcn_raw_buffer_store_b128(v, r, voff, soff, 0);
+	store_data_guard(v);
 }
 
 /* Non-temporal variants for data touched once (cache-policy bit 1: the
@@ -167,4 +176,5 @@ __device__ __forceinline__ R16 buf_load16_nt(__amdgpu_buffer_rsrc_t r, uint32_t 
 __device__ __forceinline__ void buf_store16_nt(__amdgpu_buffer_rsrc_t r, uint32_t voff, uint32_t soff, const R16 & x) {
 	const u32x4_v v = {x.w[0], x.w[1], x.w[2], x.w[3]};
 	__builtin_amdgcn_raw_buffer_store_b128(v, r, voff, soff, BUF_AUX_NT);
+	store_data_guard(v);
 }

@@ -33,9 +33,10 @@ __device__ __forceinline__ float exp_fast(float x) { return __builtin_amdgcn_exp
 
 template <typename T> __device__ __forceinline__ float rnd_in(float f) { return to_f(from_f<T>(f)); }
 
-/* Block reduction of up to two values; slots = LDS [2][16]. Ends with a
- * barrier-protected read, and the caller separates consecutive uses with
- * another barrier. */
+/* Block reductions: each wave's partial goes to its LDS cell, one barrier,
+ * then every thread reads all cells (in wave order, so the result does not
+ * depend on timing). A caller reusing the same cells must make sure every
+ * wave has finished reading them first. */
 __device__ __forceinline__ float block_max(float v, float * slots) {
 	v = wave_max(v);
 	const int nw = blockDim.x >> 6;
@@ -76,6 +77,67 @@ __device__ __forceinline__ void mean_loss_finish(int n_rows, const float * loss,
 	}
 }
 
+/* One 32-bit word of a row in storage type T: N elements. `diff` rounds
+ * x - m to T (packed, exactly as the reference's in-type subtraction) and also
+ * returns the unrounded differences and the rounded values as floats; the
+ * packed word is kept, so the output pass needs no repacking. */
+template <typename T> struct SmxWord;
+template <> struct SmxWord<bf16_t> {
+	static constexpr int N = 2;
+	__device__ static __forceinline__ void unpack(uint32_t w, float * f) { f[0] = bf16_lo(w); f[1] = bf16_hi(w); }
+	__device__ static __forceinline__ uint32_t pack(const float * f) { return pack_bf16x2(f[0], f[1]); }
+	__device__ static __forceinline__ uint32_t diff(uint32_t w, float m, float * x_m, float * d) {
+		x_m[0] = bf16_lo(w) - m;
+		x_m[1] = bf16_hi(w) - m;
+		uint32_t dw = pack_bf16x2(x_m[0], x_m[1]);
+		/* opaque, so both halves come from the one packed convert (the
+		 * compiler would otherwise convert the low half a second time) */
+		__asm__ volatile("" : "+v"(dw));
+		unpack(dw, d);
+		return dw;
+	}
+};
+template <> struct SmxWord<f16_t> {
+	static constexpr int N = 2;
+	__device__ static __forceinline__ void unpack(uint32_t w, float * f) {
+		const f16x2_v h = __builtin_bit_cast(f16x2_v, w);
+		f[0] = (float) h.x;
+		f[1] = (float) h.y;
+	}
+	__device__ static __forceinline__ uint32_t pack(const float * f) { return pack_f16x2(f[0], f[1]); }
+	__device__ static __forceinline__ uint32_t diff(uint32_t w, float m, float * x_m, float * d) {
+		float f[2];
+		unpack(w, f);
+		x_m[0] = f[0] - m;
+		x_m[1] = f[1] - m;
+		const uint32_t dw = pack_f16x2(x_m[0], x_m[1]);
+		unpack(dw, d);
+		return dw;
+	}
+};
+template <> struct SmxWord<float> {
+	static constexpr int N = 1;
+	__device__ static __forceinline__ void unpack(uint32_t w, float * f) { f[0] = __uint_as_float(w); }
+	__device__ static __forceinline__ uint32_t pack(const float * f) { return __float_as_uint(f[0]); }
+	__device__ static __forceinline__ uint32_t diff(uint32_t w, float m, float * x_m, float * d) {
+		x_m[0] = __uint_as_float(w) - m;
+		d[0] = x_m[0];
+		return __float_as_uint(d[0]);
+	}
+};
+
+/* Row max over one chunk. maximum() propagates NaN, so it needs no operand
+ * canonicalisation and folds into 3-input max instructions; a NaN anywhere in
+ * a row makes the row's sum, and so every output and the loss, NaN either way. */
+template <typename T>
+__device__ __forceinline__ float chunk_max(const R16 & r, float m) {
+	float f[VecOf<T>::N];
+	unpack16<T>(r, f);
+#pragma unroll
+	for (int e = 0; e < VecOf<T>::N; e++) m = __builtin_elementwise_maximum(m, f[e]);
+	return m;
+}
+
 /* waits for every outstanding vector-memory access of this wave
  * (s_waitcnt vmcnt(0); expcnt and lgkmcnt left at their maxima) */
 #define WAIT_VMEM_ALL() __builtin_amdgcn_s_waitcnt(0x0F70)
@@ -87,17 +149,25 @@ typedef __attribute__((address_space(3))) void * lds_ptr_t;
 /* Register-resident row path, persistent over rows (row = block, block +
  * grid, ...). Chunk c of thread t is row chunk c * blockDim + t, addressed
  * through a per-row buffer resource (one VGPR offset for all chunks); the
- * whole row sits in VGPRs. The first SMX_PF chunks of the NEXT row are
- * prefetched straight into LDS (16-byte buffer loads with the LDS bit) while
- * the current row computes, so half of each row's HBM read overlaps the
- * arithmetic of the previous row; the other half is loaded into VGPRs at the
- * top of its row, behind the previous row's stores. Each wave prefetches into and reads from
- * its own LDS slice only, so no workgroup barrier guards the buffer. */
+ * whole row sits in VGPRs. The next row is fetched while this one computes:
+ * its first SMX_PF chunks go straight into LDS (16-byte buffer loads with the
+ * LDS bit) during the max and sum passes, and each of its other chunks is
+ * loaded into chunk c's registers as soon as the output pass has stored this
+ * row's chunk c. Each wave prefetches into and reads from its own LDS slice
+ * only, so no workgroup barrier guards the buffer. */
 template <typename T, typename TO, bool FUSED>
 __device__ __forceinline__ void smx_regs(int n_rows, int n_cols, const T * X, TO * out, const uint32_t * labels, float * loss) {
 	constexpr int VEC = VecOf<T>::N;
+	using W = SmxWord<T>;
+	using WO = SmxWord<TO>;
 	static_assert(sizeof(T) == sizeof(TO), "in-register output packing needs equal widths");
-	__shared__ float slots[32];
+	/* fp32 differences are not rounded, so sum exp(d) is already sum exp(x - m) */
+	constexpr bool CORR = FUSED && sizeof(T) < 4;
+	/* separate LDS cells for the max and the sum: each is rewritten only after
+	 * every wave has passed the other reduction's barrier, so reuse needs no
+	 * barrier of its own (two barriers per row) */
+	__shared__ float mslots[16];
+	__shared__ float sslots[32];
 	__shared__ __attribute__((aligned(16))) R16 pf[SMX_PF * SMX_THREADS];
 	const int tid = threadIdx.x;
 	constexpr int nt = SMX_THREADS;          /* the launch guarantees blockDim.x == SMX_THREADS */
@@ -109,15 +179,19 @@ __device__ __forceinline__ void smx_regs(int n_rows, int n_cols, const T * X, TO
 	const uint32_t voff = (uint32_t) tid * 16u;
 
 	int row = blockIdx.x;
-	/* prologue: the LDS part of this workgroup's first row */
+	R16 xr[SMX_MAXCH];
+	/* prologue: this workgroup's first row, LDS part and register part */
 	if (row < n_rows) {
 		const __amdgpu_buffer_rsrc_t r0 = make_rsrc(X + (long) row * n_cols, row_bytes);
 #pragma unroll
 		for (int c = 0; c < SMX_PF; c++)
 			if (c < nch) __builtin_amdgcn_raw_ptr_buffer_load_lds(r0, (lds_ptr_t) &pf[c * nt + wave_base], 16, voff, c * cstride, 0, BUF_AUX_NT);
+#pragma unroll
+		for (int c = SMX_PF; c < SMX_MAXCH; c++)
+			if (c < nch) xr[c] = buf_load16_nt(r0, voff, c * cstride);
 	}
+	WAIT_VMEM_ALL();
 	for (; row < n_rows; row += gridDim.x) {
-		const __amdgpu_buffer_rsrc_t rin = make_rsrc(X + (long) row * n_cols, row_bytes);
 		const __amdgpu_buffer_rsrc_t rout = make_rsrc(out + (long) row * n_cols, row_bytes);
 		uint32_t lab = 0xffffffffu;
 		float x_lab = 0.0f;
@@ -125,21 +199,16 @@ __device__ __forceinline__ void smx_regs(int n_rows, int n_cols, const T * X, TO
 			lab = labels[row];
 			if (tid == 0 && lab < (uint32_t) n_cols) x_lab = to_f(X[(long) row * n_cols + lab]);
 		}
-		/* the register part of this row, then the prefetched part from the
-		 * wave's own LDS slice */
-		R16 xr[SMX_MAXCH];
-#pragma unroll
-		for (int c = SMX_PF; c < SMX_MAXCH; c++)
-			if (c < nch) xr[c] = buf_load16_nt(rin, voff, c * cstride);
-		WAIT_VMEM_ALL();
+		/* the LDS part of this row (landed: checked before the last output pass) */
 #pragma unroll
 		for (int c = 0; c < SMX_PF; c++)
 			if (c < nch) xr[c] = pf[c * nt + tid];
 		WAIT_LDS_ALL();
 		/* start the next row's LDS part now; it lands while this row computes */
 		const int next = row + gridDim.x;
-		if (next < n_rows) {
-			const __amdgpu_buffer_rsrc_t rn = make_rsrc(X + (long) next * n_cols, row_bytes);
+		const bool has_next = next < n_rows;
+		const __amdgpu_buffer_rsrc_t rn = make_rsrc(X + (long) (has_next ? next : row) * n_cols, has_next ? row_bytes : 0u);
+		if (has_next) {
 #pragma unroll
 			for (int c = 0; c < SMX_PF; c++)
 				if (c < nch) __builtin_amdgcn_raw_ptr_buffer_load_lds(rn, (lds_ptr_t) &pf[c * nt + wave_base], 16, voff, c * cstride, 0, BUF_AUX_NT);
@@ -148,17 +217,10 @@ __device__ __forceinline__ void smx_regs(int n_rows, int n_cols, const T * X, TO
 		float m = -__builtin_inff();
 #pragma unroll
 		for (int c = 0; c < SMX_MAXCH; c++) {
-			if (c < nch) {
-				float f[VEC];
-				unpack16<T>(xr[c], f);
-				float cm = f[0];
-#pragma unroll
-				for (int e = 1; e < VEC; e++) cm = fmaxf(cm, f[e]);
-				/* chunks past the row end hold zeros: keep them out of the max */
-				m = (c * nt + tid < nv) ? fmaxf(m, cm) : m;
-			}
+			/* chunks past the row end hold zeros: keep them out of the max */
+			if (c < nch && c * nt + tid < nv) m = chunk_max<T>(xr[c], m);
 		}
-		m = block_max(m, slots);
+		m = block_max(m, mslots);
 #pragma unroll
 		for (int c = 0; c < SMX_MAXCH; c++) reg_barrier(xr[c]);
 
@@ -170,50 +232,75 @@ __device__ __forceinline__ void smx_regs(int n_rows, int n_cols, const T * X, TO
 #pragma unroll
 		for (int c = 0; c < SMX_MAXCH; c++) {
 			if (c < nch && c * nt + tid < nv) {
-				float f[VEC];
-				unpack16<T>(xr[c], f);
+				R16 o;
 #pragma unroll
-				for (int e = 0; e < VEC; e++) {
-					const float diff = f[e] - m;
-					const float d = rnd_in<T>(diff);
-					const float ex = exp_fast(d);
-					if (e & 1) sd1 += ex; else sd0 += ex;
-					/* fmaxf drops the NaN of -inf - (-inf) (where ex is 0 anyway) */
-					if (FUSED) corr = fmaf(ex, fmaxf(diff - d, -1.0f), corr);
-					f[e] = d;
+				for (int i = 0; i < 4; i++) {
+					float x_m[W::N], d[W::N];
+					o.w[i] = W::diff(xr[c].w[i], m, x_m, d);
+#pragma unroll
+					for (int e = 0; e < W::N; e++) {
+						const float ex = exp_fast(d[e]);
+						if ((i * W::N + e) & 1) sd1 += ex; else sd0 += ex;
+						/* fmaxf drops the NaN of -inf - (-inf) (where ex is 0 anyway) */
+						if (CORR) corr = fmaf(ex, fmaxf(x_m[e] - d[e], -1.0f), corr);
+					}
 				}
-				xr[c] = pack16<T>(f);   /* d is exact in T */
+				xr[c] = o;   /* d, exact in T */
 			}
 		}
 		float sd = sd0 + sd1;
 		float sx = sd + corr;
-		__syncthreads();   /* slots reuse */
-		block_sum2(sd, sx, slots);
+		block_sum2(sd, sx, sslots);
 		/* y = exp(d) / sd as one exp2: exp2(d * log2(e) - log2(sd)) */
 		const float nlog2s = -__builtin_amdgcn_logf(sd);
+		/* the next row's LDS part is the only vector-memory traffic in flight
+		 * here (this row's loads were consumed by the max pass) */
+		WAIT_VMEM_ALL();
 
-		/* chunk and lane holding the label (if any) */
+		/* chunk and element holding the label (if any) */
 		const int lab_chunk = (lab < (uint32_t) n_cols) ? (int) (lab / VEC) : -1;
+		const int le = (int) (lab % VEC);
+		/* Output pass: the register-loaded chunks (c >= SMX_PF) first, then the
+		 * next row's loads into those registers, then the LDS-loaded chunks, so
+		 * the next row's loads queue behind half of this row's stores. */
 #pragma unroll
-		for (int c = 0; c < SMX_MAXCH; c++) {
+		for (int k = 0; k < SMX_MAXCH; k++) {
+			const int c = (k + SMX_PF) % SMX_MAXCH;
 			if (c < nch) {
-				float f[VEC];
-				unpack16<T>(xr[c], f);
+				R16 o;
 #pragma unroll
-				for (int e = 0; e < VEC; e++) f[e] = __builtin_amdgcn_exp2f(fmaf(f[e], SMX_LOG2E, nlog2s));
-				if (FUSED && (c * nt + tid) == lab_chunk) {
-					const int le = (int) (lab % VEC);
+				for (int i = 0; i < 4; i++) {
+					float f[W::N];
+					W::unpack(xr[c].w[i], f);
 #pragma unroll
-					for (int e = 0; e < VEC; e++)
-						if (e == le) f[e] = rnd_in<TO>(f[e]) - 1.0f;
+					for (int e = 0; e < W::N; e++) f[e] = __builtin_amdgcn_exp2f(fmaf(f[e], SMX_LOG2E, nlog2s));
+					o.w[i] = WO::pack(f);
 				}
-				buf_store16_nt(rout, voff, c * cstride, pack16<TO>(f));
+				/* the label's chunk: a wave-uniform branch taken by one wave per
+				 * row, so the other chunks carry no per-element label test */
+				const bool at_label = FUSED && (c * nt + tid) == lab_chunk;
+				if (FUSED && __builtin_amdgcn_ballot_w64(at_label) != 0ull) {
+#pragma unroll
+					for (int i = 0; i < 4; i++) {
+						float f[W::N];
+						WO::unpack(o.w[i], f);
+#pragma unroll
+						for (int e = 0; e < W::N; e++)
+							if (at_label && i * W::N + e == le) f[e] -= 1.0f;
+						o.w[i] = WO::pack(f);
+					}
+				}
+				buf_store16_nt(rout, voff, c * cstride, o);
+			}
+			if (k == SMX_MAXCH - SMX_PF - 1 && has_next) {
+#pragma unroll
+				for (int c2 = SMX_PF; c2 < SMX_MAXCH; c2++)
+					if (c2 < nch) xr[c2] = buf_load16_nt(rn, voff, c2 * cstride);
 			}
 		}
 		if (FUSED && tid == 0 && loss) {
 			loss[row] = (lab < (uint32_t) n_cols) ? (logf(sx) + m - x_lab) : __builtin_nanf("");
 		}
-		__syncthreads();   /* slots reuse by the next row */
 	}
 	WAIT_VMEM_ALL();
 }
