@@ -224,28 +224,27 @@ def build_extras(h, pool, api):
 
 
 def time_ops(h, hip, ops, steps, warmup):
+    """Time `steps` steps (each op once per step, rotating buffer sets) on one
+    stream. One event sits between consecutive launches, so the per-op
+    durations of a step add up exactly to the step's time."""
     stream = h.stream(0)
-    evs = {name: [(hip.event(), hip.event()) for _ in range(steps)] for name, _, _ in ops}
-    first, last = hip.event(), hip.event()
+    evs = [[hip.event() for _ in range(len(ops) + 1)] for _ in range(steps)]
     for w in range(warmup):
         for name, _, runs in ops:
             assert runs[w % len(runs)]() == 0, name
     h.sync()
     t0 = time.perf_counter()
-    hip.record(first, stream)
     for s in range(steps):
-        for name, _, runs in ops:
-            a, b = evs[name][s]
-            hip.record(a, stream)
+        hip.record(evs[s][0], stream)
+        for i, (name, _, runs) in enumerate(ops):
             assert runs[(warmup + s) % len(runs)]() == 0, name
-            hip.record(b, stream)
-    hip.record(last, stream)
+            hip.record(evs[s][i + 1], stream)
     h.sync()
     wall = time.perf_counter() - t0
-    step_ms = hip.elapsed_ms(first, last) / steps
+    step_ms = hip.elapsed_ms(evs[0][0], evs[-1][-1]) / steps
     per_op = {}
-    for name, nbytes, runs in ops:
-        t = sorted(hip.elapsed_ms(a, b) for a, b in evs[name])
+    for i, (name, nbytes, runs) in enumerate(ops):
+        t = sorted(hip.elapsed_ms(evs[s][i], evs[s][i + 1]) for s in range(steps))
         med = t[len(t) // 2]
         per_op[name] = {"bytes": nbytes, "median_us": round(med * 1e3, 2), "min_us": round(t[0] * 1e3, 2),
                         "gbps": round(nbytes / (med * 1e-3) / 1e9, 1),
