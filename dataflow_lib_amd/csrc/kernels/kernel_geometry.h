@@ -30,8 +30,9 @@
  * SMX_THREADS * SMX_MAXCH 16-byte chunks held in registers */
 #define SMX_THREADS 1024
 #define SMX_MAXCH 16
-/* chunks per thread of the next row prefetched into LDS (8 x 16 KB) */
-#define SMX_PF 8
+/* chunks per thread of the next row prefetched into LDS (9 x 16 KB); the
+ * other SMX_MAXCH - SMX_PF chunks of the next row are prefetched into VGPRs */
+#define SMX_PF 9
 
 /* RoPE: one wave per token, 4 waves per workgroup, head_dim <= 512 */
 #define ROPE_MAX_HEAD_DIM 512

@@ -178,8 +178,13 @@ __device__ __forceinline__ void smx_regs(int n_rows, int n_cols, const T * X, TO
 	const uint32_t row_bytes = (uint32_t) n_cols * (uint32_t) sizeof(T);
 	const uint32_t voff = (uint32_t) tid * 16u;
 
+	/* chunks SMX_PF .. SMX_PF + RP - 1 of the next row are loaded a row ahead
+	 * into VGPRs; fp32 rows keep those registers for temporaries and load the
+	 * chunks past SMX_PF + RP at the top of their own row */
+	constexpr int RP = sizeof(T) < 4 ? SMX_MAXCH - SMX_PF : 0;
 	int row = blockIdx.x;
 	R16 xr[SMX_MAXCH];
+	R16 nx[RP > 0 ? RP : 1];
 	/* prologue: this workgroup's first row, LDS part and register part */
 	if (row < n_rows) {
 		const __amdgpu_buffer_rsrc_t r0 = make_rsrc(X + (long) row * n_cols, row_bytes);
@@ -187,8 +192,8 @@ __device__ __forceinline__ void smx_regs(int n_rows, int n_cols, const T * X, TO
 		for (int c = 0; c < SMX_PF; c++)
 			if (c < nch) __builtin_amdgcn_raw_ptr_buffer_load_lds(r0, (lds_ptr_t) &pf[c * nt + wave_base], 16, voff, c * cstride, 0, BUF_AUX_NT);
 #pragma unroll
-		for (int c = SMX_PF; c < SMX_MAXCH; c++)
-			if (c < nch) xr[c] = buf_load16_nt(r0, voff, c * cstride);
+		for (int c = SMX_PF; c < SMX_PF + RP; c++)
+			if (c < nch) nx[c - SMX_PF] = buf_load16_nt(r0, voff, c * cstride);
 	}
 	WAIT_VMEM_ALL();
 	for (; row < n_rows; row += gridDim.x) {
@@ -199,19 +204,32 @@ __device__ __forceinline__ void smx_regs(int n_rows, int n_cols, const T * X, TO
 			lab = labels[row];
 			if (tid == 0 && lab < (uint32_t) n_cols) x_lab = to_f(X[(long) row * n_cols + lab]);
 		}
-		/* the LDS part of this row (landed: checked before the last output pass) */
+		/* this row: the LDS part (landed: checked before the last output pass)
+		 * and the register part loaded during the last row */
 #pragma unroll
 		for (int c = 0; c < SMX_PF; c++)
 			if (c < nch) xr[c] = pf[c * nt + tid];
 		WAIT_LDS_ALL();
-		/* start the next row's LDS part now; it lands while this row computes */
+#pragma unroll
+		for (int c = SMX_PF; c < SMX_PF + RP; c++)
+			if (c < nch) xr[c] = nx[c - SMX_PF];
+		if (RP < SMX_MAXCH - SMX_PF) {
+			const __amdgpu_buffer_rsrc_t rin = make_rsrc(X + (long) row * n_cols, row_bytes);
+#pragma unroll
+			for (int c = SMX_PF + RP; c < SMX_MAXCH; c++)
+				if (c < nch) xr[c] = buf_load16_nt(rin, voff, c * cstride);
+		}
+		/* the whole next row is requested now and lands while this row computes */
 		const int next = row + gridDim.x;
 		const bool has_next = next < n_rows;
-		const __amdgpu_buffer_rsrc_t rn = make_rsrc(X + (long) (has_next ? next : row) * n_cols, has_next ? row_bytes : 0u);
 		if (has_next) {
+			const __amdgpu_buffer_rsrc_t rn = make_rsrc(X + (long) next * n_cols, row_bytes);
 #pragma unroll
 			for (int c = 0; c < SMX_PF; c++)
 				if (c < nch) __builtin_amdgcn_raw_ptr_buffer_load_lds(rn, (lds_ptr_t) &pf[c * nt + wave_base], 16, voff, c * cstride, 0, BUF_AUX_NT);
+#pragma unroll
+			for (int c = SMX_PF; c < SMX_PF + RP; c++)
+				if (c < nch) nx[c - SMX_PF] = buf_load16_nt(rn, voff, c * cstride);
 		}
 
 		float m = -__builtin_inff();
@@ -253,19 +271,17 @@ __device__ __forceinline__ void smx_regs(int n_rows, int n_cols, const T * X, TO
 		block_sum2(sd, sx, sslots);
 		/* y = exp(d) / sd as one exp2: exp2(d * log2(e) - log2(sd)) */
 		const float nlog2s = -__builtin_amdgcn_logf(sd);
-		/* the next row's LDS part is the only vector-memory traffic in flight
-		 * here (this row's loads were consumed by the max pass) */
+		/* the next row's loads are the only vector-memory traffic in flight
+		 * here (issued a whole max and sum pass ago; this row's own loads were
+		 * consumed by the max pass); its LDS part must have landed before the
+		 * next row reads it */
 		WAIT_VMEM_ALL();
 
 		/* chunk and element holding the label (if any) */
 		const int lab_chunk = (lab < (uint32_t) n_cols) ? (int) (lab / VEC) : -1;
 		const int le = (int) (lab % VEC);
-		/* Output pass: the register-loaded chunks (c >= SMX_PF) first, then the
-		 * next row's loads into those registers, then the LDS-loaded chunks, so
-		 * the next row's loads queue behind half of this row's stores. */
 #pragma unroll
-		for (int k = 0; k < SMX_MAXCH; k++) {
-			const int c = (k + SMX_PF) % SMX_MAXCH;
+		for (int c = 0; c < SMX_MAXCH; c++) {
 			if (c < nch) {
 				R16 o;
 #pragma unroll
@@ -291,11 +307,6 @@ __device__ __forceinline__ void smx_regs(int n_rows, int n_cols, const T * X, TO
 					}
 				}
 				buf_store16_nt(rout, voff, c * cstride, o);
-			}
-			if (k == SMX_MAXCH - SMX_PF - 1 && has_next) {
-#pragma unroll
-				for (int c2 = SMX_PF; c2 < SMX_MAXCH; c2++)
-					if (c2 < nch) xr[c2] = buf_load16_nt(rn, voff, c2 * cstride);
 			}
 		}
 		if (FUSED && tid == 0 && loss) {
