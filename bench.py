@@ -13,10 +13,14 @@ once, on its next rotating buffer set, through the C ABI (submit_* on stream 0):
 
 Inputs are resident in HBM before timing. Each op rotates through enough
 buffer sets that its working set per rotation is >= 1 GiB, so the 256 MB
-Infinity Cache cannot serve repeats. Per-op kernel time = median of hipEvent
-pairs recorded on the launch stream; `value` = sum of per-op algorithmic bytes
-/ measured step time. The reference-compatible split ops (rms_norm_bwd_x,
-rms_norm_bwd_w, softmax, cross_entropy_loss) are timed as extras.
+Infinity Cache cannot serve repeats. Per-op time = median over steps of the
+interval between the events recorded around its launch on the launch stream
+(one event between consecutive launches); `value` = sum of per-op algorithmic
+bytes / measured step time. Timed as extras, outside `value`: the
+reference-compatible split ops (rms_norm_bwd_x, rms_norm_bwd_w, softmax,
+cross_entropy_loss) and the path's neighbours (embedding gather of 8192 rows
+of a 128256 x 4096 bf16 table; copy_to_seq_context of K, V [8192 x 1024] bf16
+into 4 contexts of 2048 positions).
 
 cpu_baseline: the C oracle (oracle/liboracle.so, OpenMP over rows, fp64
 arithmetic) on a bounded row sample of the same ops, timed on this host.
@@ -220,6 +224,27 @@ def build_extras(h, pool, api):
     labels = pool.put(np.random.default_rng(9).integers(0, V, size=R).astype(np.uint32))
     P = pool.fill(lg, "normal_bf16", 11, 0.0, 1e-3)
     ops.append(("cross_entropy_loss", R * 4 + 2 * R * 2, [lambda: api.submit_cross_entropy_loss(h, 0, BF16, R, V, P, labels)]))
+    # --- embedding gather (next to the path): 8192 token rows of a 128256 x 4096 bf16 table
+    table = pool.fill(V * D * 2, "normal_bf16", 12)
+    runs = []
+    for s in range(n_sets(2 * act)):
+        ids = pool.put(np.random.default_rng(20 + s).integers(0, V, size=T).astype(np.uint32))
+        out = pool.empty(act)
+        runs.append(lambda ids=ids, out=out: api.submit_embedding(h, 0, BF16, T, D, ids, table, out))
+    ops.append(("embedding", 2 * act + T * 4, runs))
+    # --- KV-cache scatter: 8192 tokens (4 sequences x 2048 positions) of K and V [8192 x 1024] bf16
+    kv = T * 1024 * 2
+    pos = np.arange(T, dtype=np.int32) % 2048
+    sizes = np.full(T, 2048, np.int32)
+    runs = []
+    for s in range(n_sets(4 * kv)):
+        K, Vv = pool.fill(kv, "normal_bf16", 30), pool.fill(kv, "normal_bf16", 31)
+        ctx = [pool.empty(2 * 2048 * 1024 * 2) for _ in range(4)]
+        ptrs = pool.put(np.array([ctx[t // 2048] for t in range(T)], np.uint64))
+        pp, ps = pool.put(pos), pool.put(sizes)
+        runs.append(lambda K=K, Vv=Vv, pp=pp, ptrs=ptrs, ps=ps:
+                    api.submit_copy_to_seq_context(h, 0, BF16, T * 1024, T, 1024, K, Vv, pp, ptrs, ps))
+    ops.append(("copy_to_seq_context", 4 * kv + T * (4 + 8 + 4), runs))
     return ops
 
 

@@ -145,6 +145,8 @@ def _declare(L):
     L.destroy_dataflow_handle.argtypes = [_H]
     L.register_native_ops.argtypes = [_H, ctypes.c_char_p, ctypes.c_char_p]
     h, s = _H, i
+    L.submit_embedding.argtypes = [h, s, i, i, i, vp, vp, vp]
+    L.submit_copy_to_seq_context.argtypes = [h, s, i, u64, i, i, vp, vp, vp, vp, vp]
     L.submit_rms_norm.argtypes = [h, s, i, i, i, f32, vp, vp, vp, vp, vp]
     L.submit_rms_norm_bwd_x.argtypes = [h, s, i, i, i, i, f32, vp, vp, vp, vp, vp, vp]
     L.submit_rms_norm_bwd_w.argtypes = [h, s, i, i, i, i, f32, vp, vp, vp, vp]
@@ -275,6 +277,16 @@ def submit_rms_norm_bwd(handle, stream_id, fwd_dt, bwd_dt, n_rows, n_cols, eps, 
                         upstream_dX, dX, dW):
     return lib().submit_rms_norm_bwd(_h(handle), stream_id, fwd_dt, bwd_dt, n_rows, n_cols, eps, fwd_rms_vals,
                                      rms_weight, X_inp, upstream_dX, dX, dW)
+
+
+def submit_embedding(handle, stream_id, fwd_dt, num_tokens, embed_dim, token_ids, embedding_table, output):
+    return lib().submit_embedding(_h(handle), stream_id, fwd_dt, num_tokens, embed_dim, token_ids, embedding_table, output)
+
+
+def submit_copy_to_seq_context(handle, stream_id, fwd_dt, N, total_tokens, kv_dim, X_k, X_v, seq_positions,
+                               seq_context_ptrs, seq_context_sizes):
+    return lib().submit_copy_to_seq_context(_h(handle), stream_id, fwd_dt, N, total_tokens, kv_dim, X_k, X_v,
+                                            seq_positions, seq_context_ptrs, seq_context_sizes)
 
 
 def submit_rope(handle, stream_id, fwd_dt, N, model_dim, head_dim, num_kv_heads, theta, seq_positions, X_q, X_k):

@@ -200,6 +200,46 @@ int rope_bwd_x_set_launch_config(Hip_Launch_Config * hip_launch_config, Dataflow
 	return rope_config(hip_launch_config, dataflow_handle, op, "rope bwd x");
 }
 
+/* ---------------- embedding / copy_to_seq_context ---------------- */
+
+/* one wave per row, looping; eight workgroups of GS_WAVES waves per CU */
+static void gs_config(Hip_Launch_Config * c, Dataflow_Handle * h, uint64_t n_rows) {
+	uint64_t grid = MY_CEIL(n_rows, (uint64_t) GS_WAVES);
+	grid = MY_MIN(grid, (uint64_t) dev(h)->cu_count * 8u);
+	set_1d(c, (unsigned) grid, 64 * GS_WAVES, 0);
+}
+
+/* reference: src/ops/nvidia/preprocess/embedding_config.c:3-40 */
+int embedding_set_launch_config(Hip_Launch_Config * hip_launch_config, Dataflow_Handle * dataflow_handle, Hip_Function * hip_function, Op * op) {
+	const int num_tokens = ARG(op, 0, int), embed_dim = ARG(op, 1, int);
+	const size_t elem = arg_elem_bytes(hip_function, 3);
+	if (elem == 0) {
+		fprintf(stderr, "Error: embedding not available for dtype %s...\n",
+				dataflow_datatype_as_string(hip_function->op_skeleton.header.arg_dtypes[3]));
+		return -1;
+	}
+	if (num_tokens < 0 || embed_dim < 0 || (uint64_t) embed_dim * elem > 0xffffffffull) {
+		fprintf(stderr, "Error: embedding: invalid shape (%d tokens x %d)...\n", num_tokens, embed_dim);
+		return -1;
+	}
+	gs_config(hip_launch_config, dataflow_handle, (embed_dim == 0) ? 0 : (uint64_t) num_tokens);
+	return 0;
+}
+
+/* reference: src/ops/nvidia/attention/attn_misc_config.c:56-80 */
+int copy_to_seq_context_set_launch_config(Hip_Launch_Config * hip_launch_config, Dataflow_Handle * dataflow_handle, Hip_Function * hip_function, Op * op) {
+	const uint64_t N = ARG(op, 0, uint64_t);
+	const int kv_dim = ARG(op, 2, int);
+	const size_t elem = arg_elem_bytes(hip_function, 3);
+	if (elem == 0 || kv_dim <= 0 || (N % (uint64_t) kv_dim) != 0 || (uint64_t) kv_dim * elem > 0xffffffffull) {
+		fprintf(stderr, "Error: copy to seq context: unsupported N=%lu kv_dim=%d (need kv_dim > 0 dividing N)...\n",
+				(unsigned long) N, kv_dim);
+		return -1;
+	}
+	gs_config(hip_launch_config, dataflow_handle, N / (uint64_t) kv_dim);
+	return 0;
+}
+
 /* ---------------- SwiGLU ---------------- */
 
 static int swiglu_config(Hip_Launch_Config * c, Dataflow_Handle * h, Hip_Function * f, Op * op, const char * what) {

@@ -139,22 +139,27 @@ DEFINE_FWD_SETTER(set_native_softmax_cross_entropy_loss_skeleton, "softmax_cross
 
 /* ---- registration ---- */
 
-/* Variants provided by the gfx950 code object. Ops of the reference that are
- * not part of this library (embedding, copy_to_seq_context) and the fp8
- * variants are absent; submit_op reports them as unknown fingerprints. */
+/* Variants provided by the gfx950 code object. The reference's fp8 variants
+ * of the arithmetic ops are absent (submit_op reports them as unknown
+ * fingerprints); embedding and copy_to_seq_context move bytes only, so they
+ * come in every storage type the reference registers, fp8 included. */
 typedef struct { const char * op; DataflowDatatype fwd; DataflowDatatype bwd; } Native_Variant;
 
 #define FWD3(op) {op, DATAFLOW_FP32, DATAFLOW_NONE}, {op, DATAFLOW_FP16, DATAFLOW_NONE}, {op, DATAFLOW_BF16, DATAFLOW_NONE}
 #define BWD3(op) {op, DATAFLOW_NONE, DATAFLOW_FP32}, {op, DATAFLOW_NONE, DATAFLOW_FP16}, {op, DATAFLOW_NONE, DATAFLOW_BF16}
 #define PAIR3(op) {op, DATAFLOW_FP32, DATAFLOW_FP32}, {op, DATAFLOW_FP16, DATAFLOW_FP16}, {op, DATAFLOW_BF16, DATAFLOW_BF16}
 
+#define FWD5(op) FWD3(op), {op, DATAFLOW_FP8E4M3, DATAFLOW_NONE}, {op, DATAFLOW_FP8E5M2, DATAFLOW_NONE}
+
 static const Native_Variant native_variants[] = {
+	FWD5("embedding"),
 	FWD3("rms_norm"),
 	PAIR3("rms_norm_bwd_x"),
 	PAIR3("rms_norm_bwd_w"),
 	PAIR3("rms_norm_bwd"),
 	FWD3("rope"),
 	BWD3("rope_bwd_x"),
+	FWD5("copy_to_seq_context"),
 	FWD3("swiglu"),
 	PAIR3("swiglu_bwd_x"),
 	PAIR3("softmax"),

@@ -7,3 +7,4 @@
 #include "rope.hip"
 #include "swiglu.hip"
 #include "softmax_xent.hip"
+#include "gather_scatter.hip"

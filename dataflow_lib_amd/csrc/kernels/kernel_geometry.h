@@ -38,6 +38,9 @@
 #define ROPE_MAX_HEAD_DIM 512
 #define ROPE_WAVES 4
 
+/* embedding / copy_to_seq_context: one wave per row, 4 waves per workgroup */
+#define GS_WAVES 4
+
 /* SwiGLU: grid-stride, one 512-thread workgroup per CU, 16-byte chunks per
  * thread in flight */
 #define SWIGLU_UNROLL 4

@@ -1,8 +1,8 @@
 /*
  * Op API: build an Op on the stack (skeleton + pointers to each argument, in
  * skeleton order) and submit it. Argument order and meaning follow the
- * reference's src/dataflow_ops/src/{norm_ops.c:4-97, attn_misc_ops.c:3-65,
- * mlp_misc_ops.c:3-61, loss_misc_ops.c:4-60}.
+ * reference's src/dataflow_ops/src/{preprocess_ops.c:3-32, norm_ops.c:4-97,
+ * attn_misc_ops.c:3-100, mlp_misc_ops.c:3-61, loss_misc_ops.c:4-60}.
  */
 #include "dataflow_ops.h"
 
@@ -16,6 +16,18 @@ static int submit_built_op(Dataflow_Handle * handle, Op * op, int stream_id, con
 		return -1;
 	}
 	return 0;
+}
+
+int submit_embedding(Dataflow_Handle * handle, int stream_id,
+						DataflowDatatype fwd_dt,
+						int num_tokens, int embed_dim,
+						uint32_t * token_ids, void * embedding_table, void * output) {
+	Op op;
+	set_native_embedding_skeleton(&op.op_skeleton, fwd_dt);
+	void ** a = op.op_args;
+	a[0] = &num_tokens; a[1] = &embed_dim;
+	a[2] = &token_ids; a[3] = &embedding_table; a[4] = &output;
+	return submit_built_op(handle, &op, stream_id, "embedding");
 }
 
 int submit_rms_norm(Dataflow_Handle * handle, int stream_id,
@@ -94,6 +106,18 @@ int submit_rope_bwd_x(Dataflow_Handle * handle, int stream_id,
 	a[0] = &N; a[1] = &model_dim; a[2] = &head_dim; a[3] = &num_kv_heads; a[4] = &theta;
 	a[5] = &seq_positions; a[6] = &dX_q; a[7] = &dX_k;
 	return submit_built_op(handle, &op, stream_id, "rope bwd x");
+}
+
+int submit_copy_to_seq_context(Dataflow_Handle * handle, int stream_id,
+						DataflowDatatype fwd_dt,
+						uint64_t N, int total_tokens, int kv_dim,
+						void * X_k, void * X_v, int * seq_positions, uint64_t * seq_context_ptrs, int * seq_context_sizes) {
+	Op op;
+	set_native_copy_to_seq_context_skeleton(&op.op_skeleton, fwd_dt);
+	void ** a = op.op_args;
+	a[0] = &N; a[1] = &total_tokens; a[2] = &kv_dim;
+	a[3] = &X_k; a[4] = &X_v; a[5] = &seq_positions; a[6] = &seq_context_ptrs; a[7] = &seq_context_sizes;
+	return submit_built_op(handle, &op, stream_id, "copy to seq context");
 }
 
 int submit_swiglu(Dataflow_Handle * handle, int stream_id,

@@ -17,6 +17,16 @@
 extern "C" {
 #endif
 
+/* --- preprocess (reference: src/dataflow_ops/src/preprocess_ops.c:3-32) --- */
+
+/* output[t, :] = embedding_table[token_ids[t], :] for t < num_tokens (rows of
+ * embed_dim elements of fwd_dt; every storage type incl. fp8). Token ids must
+ * index rows of the table, as in the reference. */
+int submit_embedding(Dataflow_Handle * handle, int stream_id,
+						DataflowDatatype fwd_dt,
+						int num_tokens, int embed_dim,
+						uint32_t * token_ids, void * embedding_table, void * output);
+
 /* --- norm (reference: src/dataflow_ops/src/norm_ops.c:4-97) --- */
 
 /* out = (X * rstd) * w per row; weighted_sums[r] = sum_j X*w, rms_vals[r] = rstd
@@ -62,6 +72,15 @@ int submit_rope_bwd_x(Dataflow_Handle * handle, int stream_id,
 						DataflowDatatype bwd_dt,
 						uint64_t N, int model_dim, int head_dim, int num_kv_heads, int theta,
 						int * seq_positions, void * dX_q, void * dX_k);
+
+/* KV-cache scatter (reference: attn_misc_ops.c:69-100): for token t <
+ * N / kv_dim, with ctx = (fwd_dt *) seq_context_ptrs[t], p = seq_positions[t]
+ * and S = seq_context_sizes[t], row t of X_k goes to ctx row p and row t of X_v
+ * to ctx row S + p (a context holds S key rows, then S value rows). */
+int submit_copy_to_seq_context(Dataflow_Handle * handle, int stream_id,
+						DataflowDatatype fwd_dt,
+						uint64_t N, int total_tokens, int kv_dim,
+						void * X_k, void * X_v, int * seq_positions, uint64_t * seq_context_ptrs, int * seq_context_sizes);
 
 /* --- mlp misc (reference: src/dataflow_ops/src/mlp_misc_ops.c:3-61) --- */
 

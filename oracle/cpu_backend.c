@@ -230,6 +230,25 @@ static int softmax_xent_adapter(int dt, void ** op_args) {
 	return ret;
 }
 
+static int embedding_adapter(int elem_bytes, void ** op_args) {
+	return oracle_embedding(elem_bytes, A(0, int), A(1, int), A(2, uint32_t *), A(3, void *), -1, A(4, void *));
+}
+
+static int copy_to_seq_context_adapter(int elem_bytes, void ** op_args) {
+	return oracle_copy_to_seq_context(elem_bytes, A(0, uint64_t), A(2, int), A(3, void *), A(4, void *), A(5, int *),
+										A(6, uint64_t *), A(7, int *));
+}
+
+#define ADAPT_MOVE(sfx, bytes)                                                                              \
+	int embedding_##sfx##_kernel(void ** a) { return embedding_adapter(bytes, a); }                        \
+	int copy_to_seq_context_##sfx##_kernel(void ** a) { return copy_to_seq_context_adapter(bytes, a); }
+
+ADAPT_MOVE(fp32, 4)
+ADAPT_MOVE(fp16, 2)
+ADAPT_MOVE(bf16, 2)
+ADAPT_MOVE(fp8e4m3, 1)
+ADAPT_MOVE(fp8e5m2, 1)
+
 #define ADAPT_DT(sfx, pair, code)                                                                          \
 	int rms_norm_##sfx##_kernel(void ** a) { return rms_norm_adapter(code, a); }                           \
 	int rms_norm_bwd_x_##pair##_kernel(void ** a) { return rms_norm_bwd_x_adapter(code, a); }              \

@@ -452,3 +452,33 @@ int oracle_softmax_cross_entropy_exact(int dt, int n_rows, int n_cols, const voi
 								double * y, double * loss, double * mean_loss) {
 	return softmax_xent_impl(dt, n_rows, n_cols, X, labels, y, NULL, loss, mean_loss, 0.0);
 }
+
+/* ---------------- embedding / copy_to_seq_context ---------------- */
+
+/* reference: src/ops/nvidia/preprocess/embedding.cu:3-119, with the row
+ * offset taken in elements (the reference's typed-pointer index multiplies
+ * it by the element size once more, :14-20) */
+int oracle_embedding(int elem_bytes, int num_tokens, int embed_dim, const uint32_t * ids, const void * table, long vocab, void * out) {
+	if ((elem_bytes != 1 && elem_bytes != 2 && elem_bytes != 4) || num_tokens < 0 || embed_dim < 0) return -1;
+	const size_t row = (size_t) embed_dim * (size_t) elem_bytes;
+	for (int t = 0; t < num_tokens; t++) {
+		if (vocab >= 0 && (long) ids[t] >= vocab) return -1;
+		memcpy((char *) out + (size_t) t * row, (const char *) table + (size_t) ids[t] * row, row);
+	}
+	return 0;
+}
+
+/* reference: src/ops/nvidia/attention/copy_to_seq_context.cu:3-100 */
+int oracle_copy_to_seq_context(int elem_bytes, uint64_t N, int kv_dim, const void * keys, const void * values,
+					const int * seq_positions, const uint64_t * ctx_ptrs, const int * ctx_sizes) {
+	if ((elem_bytes != 1 && elem_bytes != 2 && elem_bytes != 4) || kv_dim <= 0 || N % (uint64_t) kv_dim) return -1;
+	const size_t row = (size_t) kv_dim * (size_t) elem_bytes;
+	const long n_tokens = (long) (N / (uint64_t) kv_dim);
+	for (long t = 0; t < n_tokens; t++) {
+		char * ctx = (char *) (uintptr_t) ctx_ptrs[t];
+		const size_t p = (size_t) seq_positions[t], S = (size_t) ctx_sizes[t];
+		memcpy(ctx + p * row, (const char *) keys + (size_t) t * row, row);
+		memcpy(ctx + (S + p) * row, (const char *) values + (size_t) t * row, row);
+	}
+	return 0;
+}

@@ -49,6 +49,15 @@ int oracle_cross_entropy_loss(int dt, int n_rows, int n_cols, void * P, const ui
 int oracle_softmax_cross_entropy(int dt, int n_rows, int n_cols, const void * X, const uint32_t * labels,
 					double * y_lo, double * y_hi, double * loss, double * mean_loss);
 
+/* byte movement (elem_bytes = 1, 2 or 4; no rounding involved):
+ * embedding: out[t, :] = table[ids[t], :]; vocab < 0 leaves ids unchecked,
+ * else an id >= vocab returns -1.
+ * copy_to_seq_context: row t of keys / values to rows p and S + p of the
+ * context at ctx_ptrs[t] (host addresses). */
+int oracle_embedding(int elem_bytes, int num_tokens, int embed_dim, const uint32_t * ids, const void * table, long vocab, void * out);
+int oracle_copy_to_seq_context(int elem_bytes, uint64_t N, int kv_dim, const void * keys, const void * values,
+					const int * seq_positions, const uint64_t * ctx_ptrs, const int * ctx_sizes);
+
 /* exact rounding chains (no evaluation slack) */
 int oracle_rms_norm_bwd_x_exact(int dt, int n_rows, int n_cols, const float * ws, const float * rs,
 					const void * W, const void * X, const void * dY, const void * dX_in, double * v);

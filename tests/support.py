@@ -40,6 +40,8 @@ def oracle():
         L.oracle_softmax.argtypes = [i, i, i, i, vp, vp]
         L.oracle_cross_entropy_loss.argtypes = [i, i, i, vp, vp]
         L.oracle_softmax_cross_entropy.argtypes = [i, i, i, vp, vp, vp, vp, vp, vp]
+        L.oracle_embedding.argtypes = [i, i, i, vp, vp, ctypes.c_long, vp]
+        L.oracle_copy_to_seq_context.argtypes = [i, ctypes.c_uint64, i, vp, vp, vp, vp, vp]
         L.oracle_load.argtypes = [i, vp, ctypes.c_long, vp]
         L.oracle_store.argtypes = [i, vp, ctypes.c_long, vp]
         _oracle = L

@@ -28,7 +28,8 @@ def cpu_handle():
 
 def test_registers_every_variant(cpu_handle):
     h, n = cpu_handle
-    assert n == 33 and h.num_ops == 33 and h.op_table.cnt == 33
+    # 11 arithmetic ops x fp32/fp16/bf16, plus embedding and copy_to_seq_context x 5 storage types
+    assert n == 43 and h.num_ops == 43 and h.op_table.cnt == 43
 
 
 def test_config1_rms_norm_fp32_through_handle(cpu_handle):
@@ -102,3 +103,28 @@ def test_other_ops_through_handle(cpu_handle, op):
         rs, dW = np.ones(3, np.float32), np.zeros(32, np.float32)
         assert api.submit_rms_norm_bwd(H, 0, FP32, FP32, 3, 32, 1e-5, ptr(rs), ptr(W), ptr(X), ptr(dY), ptr(dX), ptr(dW)) == 0
         assert np.allclose(dW, (dY * X).sum(axis=0), rtol=1e-6)
+
+
+def test_embedding_and_kv_scatter_through_handle(cpu_handle):
+    """submit_embedding / submit_copy_to_seq_context marshal their arguments
+    the way the kernels read them (fp8 variants move bytes)."""
+    h, _ = cpu_handle
+    vocab, dim = 40, 16
+    table = rng_u8(300, (vocab, dim))
+    ids = np.array([3, 0, 39, 3, 17], np.uint32)
+    out = np.zeros((ids.size, dim), np.uint8)
+    assert api.submit_embedding(ctypes.byref(h), 0, api.DATAFLOW_FP8E4M3, ids.size, dim, ptr(ids), ptr(table), ptr(out)) == 0
+    assert np.array_equal(out, table[ids])
+    kv_dim, n_tok, S = 8, 4, 6
+    ctx = np.zeros((2 * S, kv_dim), np.uint16)
+    K, V = rng_u8(301, (n_tok, 2 * kv_dim)).view(np.uint16), rng_u8(302, (n_tok, 2 * kv_dim)).view(np.uint16)
+    pos = np.array([0, 3, 1, 5], np.int32)
+    ptrs = np.full(n_tok, ctx.ctypes.data, np.uint64)
+    sizes = np.full(n_tok, S, np.int32)
+    assert api.submit_copy_to_seq_context(ctypes.byref(h), 0, BF16, n_tok * kv_dim, n_tok, kv_dim, ptr(K), ptr(V), ptr(pos),
+                                          ptr(ptrs), ptr(sizes)) == 0
+    assert np.array_equal(ctx[pos], K) and np.array_equal(ctx[S + pos], V)
+
+
+def rng_u8(seed, shape):
+    return np.random.default_rng(seed).integers(0, 256, size=shape).astype(np.uint8)

@@ -50,13 +50,15 @@ def test_every_declared_symbol_is_exported():
 
 def test_parser_sees_the_op_api():
     names = declared_functions(os.path.join(INCLUDE, "dataflow_ops.h"))
-    assert {"submit_rms_norm", "submit_rope_bwd_x", "submit_softmax_cross_entropy_loss"} <= set(names)
-    assert len(names) == 11
+    assert {"submit_rms_norm", "submit_rope_bwd_x", "submit_softmax_cross_entropy_loss", "submit_embedding",
+            "submit_copy_to_seq_context"} <= set(names)
+    assert len(names) == 13
 
 
 def test_kernel_code_object_present():
     data = open(api.KERNELS, "rb").read()
     assert data[:4] == b"\x7fELF" or data.startswith(b"__CLANG_OFFLOAD_BUNDLE__")
     for sym in (b"rms_norm_bf16_kernel", b"rms_norm_bwd_bf16_bf16_kernel_finish", b"rope_bwd_x_bf16_kernel",
-                b"swiglu_bwd_x_bf16_bf16_kernel", b"softmax_cross_entropy_loss_bf16_kernel"):
+                b"swiglu_bwd_x_bf16_bf16_kernel", b"softmax_cross_entropy_loss_bf16_kernel", b"embedding_fp8e5m2_kernel",
+                b"copy_to_seq_context_bf16_kernel"):
         assert sym in data

@@ -423,3 +423,71 @@ def test_unknown_variant_and_bad_stream(hdl):
         # fp8 RMSNorm is a reference variant this library does not provide
         assert api.submit_rms_norm(hdl, 0, api.DATAFLOW_FP8E4M3, 1, 16, 1e-5, p, p, p, None, None) == -1
         assert api.submit_swiglu(hdl, 7, BF16, 1, 8, p, p, p) == -1
+
+
+# ---------------- embedding / copy_to_seq_context (byte movement) ----------------
+
+MOVE_DTS = [(FP32, np.uint32), (FP16, np.uint16), (BF16, np.uint16), (6, np.uint8), (7, np.uint8)]   # 6, 7: FP8E4M3, FP8E5M2
+MOVE_IDS = ["fp32", "fp16", "bf16", "fp8e4m3", "fp8e5m2"]
+
+
+def rand_bits(seed, shape, np_t):
+    return rng(seed).integers(0, np.iinfo(np_t).max, size=shape, endpoint=True, dtype=np_t)
+
+
+@pytest.mark.parametrize("dt_np", MOVE_DTS, ids=MOVE_IDS)
+@pytest.mark.parametrize("shape", [(300, 64, 4096), (17, 1000, 1001), (5, 3, 8), (0, 10, 16)], ids=lambda s: "%dx%dx%d" % s)
+def test_embedding(hdl, dt_np, shape):
+    """out[t] = table[ids[t]], bit for bit (vector path when rows are 16-byte
+    multiples, element path otherwise), against the oracle's gather."""
+    from dataflow_lib_amd import api
+    dt, np_t = dt_np
+    n_tok, vocab, dim = shape
+    table = rand_bits(400, (vocab, dim), np_t)
+    ids = rng(401).integers(0, vocab, size=max(n_tok, 1)).astype(np.uint32)[:n_tok]
+    if n_tok >= 3:
+        ids[0], ids[1], ids[2] = 0, vocab - 1, 0
+    expect = np.zeros((n_tok, dim), np_t)
+    assert oracle().oracle_embedding(np.dtype(np_t).itemsize, n_tok, dim, ptr(ids), ptr(table), vocab, ptr(expect)) == 0
+    for off in (0, np.dtype(np_t).itemsize):   # aligned, then a table that is not 16-byte aligned
+        with Dev(hdl) as d:
+            pt, pi = d.put(table, offset_bytes=off), d.put(ids if n_tok else np.zeros(1, np.uint32))
+            po = d.put(np.zeros((max(n_tok, 1), dim), np_t))
+            assert api.submit_embedding(hdl, 0, dt, n_tok, dim, pi, pt, po) == 0
+            out = d.get(po, (max(n_tok, 1), dim), np_t)[:n_tok]
+        assert np.array_equal(out, expect), "embedding offset %d" % off
+
+
+@pytest.mark.parametrize("dt_np", MOVE_DTS, ids=MOVE_IDS)
+@pytest.mark.parametrize("kv_dim", [1024, 100, 8])
+def test_copy_to_seq_context(hdl, dt_np, kv_dim):
+    """Keys to row p, values to row S + p of each token's context; every other
+    context row keeps its sentinel; several tokens share a context, as the
+    tokens of one sequence do."""
+    from dataflow_lib_amd import api
+    dt, np_t = dt_np
+    seqs = [(6, [0, 1, 2, 5]), (9, [3, 0, 8]), (2, [1])]        # (S, positions of its tokens)
+    which = np.array([i for i, (_, ps) in enumerate(seqs) for _ in ps])
+    pos = np.array([p for _, ps in seqs for p in ps], np.int32)
+    sizes = np.array([seqs[w][0] for w in which], np.int32)
+    n_tok = pos.size
+    K, V = rand_bits(410, (n_tok, kv_dim), np_t), rand_bits(411, (n_tok, kv_dim), np_t)
+    sentinel = np.array(0x5A5A5A5A, np.uint32).astype(np_t)
+    host_ctx = [np.full((2 * S, kv_dim), sentinel, np_t) for S, _ in seqs]
+    host_ptrs = np.array([host_ctx[w].ctypes.data for w in which], np.uint64)
+    assert oracle().oracle_copy_to_seq_context(np.dtype(np_t).itemsize, n_tok * kv_dim, kv_dim, ptr(K), ptr(V), ptr(pos),
+                                               ptr(host_ptrs), ptr(sizes)) == 0
+    with Dev(hdl) as d:
+        dev_ctx = [d.put(np.full((2 * S, kv_dim), sentinel, np_t), offset_bytes=(0 if kv_dim % 16 == 0 else np.dtype(np_t).itemsize * (i + 1)))
+                   for i, (S, _) in enumerate(seqs)]
+        pptr = d.put(np.array([dev_ctx[w] for w in which], np.uint64))
+        pk, pv, pp, ps = d.put(K), d.put(V), d.put(pos), d.put(sizes)
+        assert api.submit_copy_to_seq_context(hdl, 0, dt, n_tok * kv_dim, n_tok, kv_dim, pk, pv, pp, pptr, ps) == 0
+        got = [d.get(p, (2 * S, kv_dim), np_t) for p, (S, _) in zip(dev_ctx, seqs)]
+    for g, e in zip(got, host_ctx):
+        assert np.array_equal(g, e)
+
+
+def test_copy_to_seq_context_rejects_ragged_n(hdl):
+    from dataflow_lib_amd import api
+    assert api.submit_copy_to_seq_context(hdl, 0, BF16, 1000, 1, 64, 0, 0, 0, 0, 0) == -1

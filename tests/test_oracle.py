@@ -297,3 +297,59 @@ def test_cross_entropy_and_fused_loss():
     P = to_storage(np.array([[0.25, 0.5], [0.125, 0.75]], np.float32), BF16)
     assert O.oracle_cross_entropy_loss(BF16, 2, 2, ptr(P), ptr(np.array([1, 7], np.uint32))) == 0
     assert np.array_equal(bf16_bits_to_f32(P), np.array([[0.25, -0.5], [0.125, 0.75]], np.float32))
+
+
+def test_embedding_gathers_rows():
+    """Rows that encode their own index come back as the token ids; gathering
+    every id in order reproduces the table; a permutation is undone by its
+    inverse; an out-of-range id is refused when the vocabulary is known."""
+    O = oracle()
+    vocab, dim = 50, 7
+    table = (np.arange(vocab, dtype=np.float32)[:, None] * 1000 + np.arange(dim, dtype=np.float32)).astype(np.float32)
+    ids = rng(200).integers(0, vocab, size=33).astype(np.uint32)
+    out = np.empty((ids.size, dim), np.float32)
+    assert O.oracle_embedding(4, ids.size, dim, ptr(ids), ptr(table), vocab, ptr(out)) == 0
+    assert np.array_equal(np.floor(out[:, 0] / 1000).astype(np.uint32), ids)
+    assert np.array_equal(out - out[:, :1], np.tile(np.arange(dim, dtype=np.float32), (ids.size, 1)))
+    every = np.arange(vocab, dtype=np.uint32)
+    full = np.empty_like(table)
+    assert O.oracle_embedding(4, vocab, dim, ptr(every), ptr(table), vocab, ptr(full)) == 0
+    assert np.array_equal(full, table)
+    perm = rng(201).permutation(vocab).astype(np.uint32)
+    once, back = np.empty_like(table), np.empty_like(table)
+    assert O.oracle_embedding(4, vocab, dim, ptr(perm), ptr(table), vocab, ptr(once)) == 0
+    assert O.oracle_embedding(4, vocab, dim, ptr(np.argsort(perm).astype(np.uint32)), ptr(once), vocab, ptr(back)) == 0
+    assert np.array_equal(back, table)
+    # 1- and 2-byte elements move the same bytes
+    b8 = table.view(np.uint8).reshape(vocab, dim * 4)
+    o8 = np.empty((ids.size, dim * 4), np.uint8)
+    assert O.oracle_embedding(1, ids.size, dim * 4, ptr(ids), ptr(b8), vocab, ptr(o8)) == 0
+    assert np.array_equal(o8.view(np.float32).reshape(out.shape), out)
+    bad = ids.copy()
+    bad[5] = vocab
+    assert O.oracle_embedding(4, bad.size, dim, ptr(bad), ptr(table), vocab, ptr(out)) == -1
+
+
+def test_copy_to_seq_context_places_keys_then_values():
+    """Keys land at row p and values at row S + p of each token's context; no
+    other row changes; reading the rows back returns the inputs."""
+    O = oracle()
+    kv_dim, n_tok = 6, 9
+    sizes = np.array([5, 5, 5, 8, 8, 8, 8, 3, 3], np.int32)
+    which = np.array([0, 0, 0, 1, 1, 1, 1, 2, 2])            # three sequences
+    pos = np.array([0, 1, 4, 0, 2, 5, 7, 2, 0], np.int32)
+    ctxs = [np.full((2 * s, kv_dim), -7.0, np.float32) for s in (5, 8, 3)]
+    ptrs = np.array([ctxs[w].ctypes.data for w in which], np.uint64)
+    K = normal(210, (n_tok, kv_dim))
+    V = normal(211, (n_tok, kv_dim))
+    assert O.oracle_copy_to_seq_context(4, n_tok * kv_dim, kv_dim, ptr(K), ptr(V), ptr(pos), ptr(ptrs), ptr(sizes)) == 0
+    touched = [set() for _ in ctxs]
+    for t in range(n_tok):
+        c, S = ctxs[which[t]], sizes[t]
+        assert np.array_equal(c[pos[t]], K[t]) and np.array_equal(c[S + pos[t]], V[t])
+        touched[which[t]] |= {int(pos[t]), int(S + pos[t])}
+    for c, tset in zip(ctxs, touched):
+        for r in range(c.shape[0]):
+            if r not in tset:
+                assert np.all(c[r] == -7.0)
+    assert O.oracle_copy_to_seq_context(4, n_tok * kv_dim + 1, kv_dim, ptr(K), ptr(V), ptr(pos), ptr(ptrs), ptr(sizes)) == -1
