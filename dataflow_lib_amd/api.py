@@ -20,6 +20,7 @@ LIB_DIR = os.path.join(PKG, "lib")
 CORE_LIB = os.path.join(LIB_DIR, "libdataflow.so")
 CONFIG_LIB = os.path.join(LIB_DIR, "libdataflow_hip_config.so")
 KERNELS = os.path.join(LIB_DIR, "dataflow_kernels_gfx950.hsaco")
+MATMUL_LIB = os.path.join(LIB_DIR, "libdataflow_hipblaslt.so")
 
 # ---- enums (values are part of op fingerprints; never reorder) ----
 DATAFLOW_NONE, DATAFLOW_VOID, DATAFLOW_FP64, DATAFLOW_FP32, DATAFLOW_FP16, DATAFLOW_BF16 = range(6)
@@ -145,6 +146,9 @@ def _declare(L):
     L.destroy_dataflow_handle.argtypes = [_H]
     L.register_native_ops.argtypes = [_H, ctypes.c_char_p, ctypes.c_char_p]
     h, s = _H, i
+    L.register_external_matmul.argtypes = [_H, ctypes.c_char_p]
+    L.submit_matmul.argtypes = [h, s, i, i, i, i, i, i, i, i, i, i, f32, f32, vp, vp, vp, vp, u64, vp]
+    L.submit_transformer_head.argtypes = [h, s, s] + [vp] * 8
     L.submit_embedding.argtypes = [h, s, i, i, i, vp, vp, vp]
     L.submit_copy_to_seq_context.argtypes = [h, s, i, u64, i, i, vp, vp, vp, vp, vp]
     L.submit_rms_norm.argtypes = [h, s, i, i, i, f32, vp, vp, vp, vp, vp]
@@ -183,7 +187,7 @@ def header_bytes(sk):
 class Handle:
     """A Dataflow_Handle on one AMD GPU (COMPUTE_HSA) with the native ops registered."""
 
-    def __init__(self, device_id=0, num_streams=1, register=True):
+    def __init__(self, device_id=0, num_streams=1, register=True, matmul=False):
         self.h = DataflowHandle()
         L = lib()
         if L.init_dataflow_handle(ctypes.byref(self.h), COMPUTE_HSA, device_id, 0, 0, num_streams, None, None) != 0:
@@ -196,6 +200,10 @@ class Handle:
             if n <= 0:
                 raise RuntimeError("register_native_ops failed (%d)" % n)
             self.num_registered = n
+        if matmul:
+            if L.register_external_matmul(ctypes.byref(self.h), MATMUL_LIB.encode()) != 1:
+                raise RuntimeError("register_external_matmul failed (%s)" % MATMUL_LIB)
+            self.num_registered += 1
 
     @property
     def ref(self):
@@ -277,6 +285,49 @@ def submit_rms_norm_bwd(handle, stream_id, fwd_dt, bwd_dt, n_rows, n_cols, eps, 
                         upstream_dX, dX, dW):
     return lib().submit_rms_norm_bwd(_h(handle), stream_id, fwd_dt, bwd_dt, n_rows, n_cols, eps, fwd_rms_vals,
                                      rms_weight, X_inp, upstream_dX, dX, dW)
+
+
+def submit_matmul(handle, stream_id, a_dt, b_dt, c_dt, d_dt, compute_dt, to_trans_a, to_trans_b, M, K, N, alpha, beta,
+                  A, B, C, D, workspaceBytes, workspace):
+    return lib().submit_matmul(_h(handle), stream_id, a_dt, b_dt, c_dt, d_dt, compute_dt, to_trans_a, to_trans_b, M, K, N,
+                               alpha, beta, A, B, C, D, workspaceBytes, workspace)
+
+
+class EmbeddingConfig(ctypes.Structure):
+    _fields_ = [("vocab_size", ctypes.c_int), ("embedding_size", ctypes.c_int)]
+
+
+class TransformerHead(ctypes.Structure):
+    """transformer_head.h (layout of the reference's Transformer_Head)"""
+    _fields_ = [("fwd_dt", ctypes.c_int), ("bwd_dt", ctypes.c_int), ("compute_dt", ctypes.c_int), ("eps", ctypes.c_float),
+                ("embedding_config", EmbeddingConfig), ("buffer", ctypes.c_void_p), ("w_head_norm", ctypes.c_void_p),
+                ("w_head", ctypes.c_void_p)]
+
+
+class TransformerHeadActivations(ctypes.Structure):
+    _fields_ = [("num_tokens", ctypes.c_int), ("buffer", ctypes.c_void_p), ("head_norm_out", ctypes.c_void_p),
+                ("head_norm_weighted_sums", ctypes.c_void_p), ("head_norm_rms_vals", ctypes.c_void_p),
+                ("head_out", ctypes.c_void_p), ("kernel_workspace", ctypes.c_void_p),
+                ("kernel_workspaceBytes", ctypes.c_uint64)]
+
+
+class TransformerBlockTransition(ctypes.Structure):
+    _fields_ = [("batch_config", ctypes.c_void_p), ("X", ctypes.c_void_p)]
+
+
+class TransformerModelOutput(ctypes.Structure):
+    _fields_ = [("batch_config", ctypes.c_void_p), ("token_ids", ctypes.c_void_p), ("labels", ctypes.c_void_p),
+                ("logits", ctypes.c_void_p), ("loss", ctypes.c_void_p), ("loss_avg", ctypes.c_float)]
+
+
+def submit_transformer_head(handle, compute_stream_id, out_copy_stream_id, block_input, transformer_head, head_activations,
+                            model_output, grad_transformer_head=None, grad_head_activations=None, grad_stream=None,
+                            next_grad_stream=None):
+    ref = lambda x: None if x is None else ctypes.cast(ctypes.byref(x), ctypes.c_void_p)
+    return lib().submit_transformer_head(_h(handle), compute_stream_id, out_copy_stream_id, ref(block_input),
+                                         ref(transformer_head), ref(head_activations), ref(model_output),
+                                         ref(grad_transformer_head), ref(grad_head_activations), ref(grad_stream),
+                                         ref(next_grad_stream))
 
 
 def submit_embedding(handle, stream_id, fwd_dt, num_tokens, embed_dim, token_ids, embedding_table, output):

@@ -5,6 +5,7 @@ Outputs (in-tree, under dataflow_lib_amd/lib/):
                                  submit_* op API and the HIP backend of Dataflow_Handle
   libdataflow_hip_config.so      launch configurations (dlopen'ed by the backend)
   dataflow_kernels_gfx950.hsaco  gfx950 code object (hipModuleLoad'ed by the backend)
+  libdataflow_hipblaslt.so       the external matmul op on hipBLASLt (register_external_matmul)
 """
 import os
 import shutil
@@ -24,6 +25,8 @@ ARCH = "gfx950"
 KERNELS_OUT = os.path.join(LIB, "dataflow_kernels_gfx950.hsaco")
 CORE_OUT = os.path.join(LIB, "libdataflow.so")
 CONFIG_OUT = os.path.join(LIB, "libdataflow_hip_config.so")
+MATMUL_OUT = os.path.join(LIB, "libdataflow_hipblaslt.so")
+CXX = os.environ.get("CXX", "g++")
 
 C_FLAGS = ["-O2", "-fPIC", "-std=gnu11", "-Wall", "-Wextra", "-Wno-unused-parameter", "-Wno-stringop-truncation",
            "-D__HIP_PLATFORM_AMD__", "-I", INCLUDE, "-I", os.path.join(CSRC, "kernels"),
@@ -74,7 +77,11 @@ def build(verbose=False):
                                       ["-o", o, "-lcrypto", "-ldl", "-lpthread"] + HIP_LINK, verbose))
     _atomic(CONFIG_OUT, lambda o: _run([CC, "-shared"] + C_FLAGS + _sources("config") +
                                         ["-o", o, "-L", LIB, "-ldataflow", "-Wl,-rpath,$ORIGIN"] + HIP_LINK, verbose))
-    return {"kernels": KERNELS_OUT, "core": CORE_OUT, "config": CONFIG_OUT}
+    _atomic(MATMUL_OUT, lambda o: _run([CXX, "-shared", "-O2", "-fPIC", "-std=c++17", "-Wall", "-D__HIP_PLATFORM_AMD__",
+                                        "-I", INCLUDE, "-I", os.path.join(ROCM, "include"),
+                                        os.path.join(CSRC, "external", "hipblaslt_matmul.cpp"), "-o", o,
+                                        "-L", os.path.join(ROCM, "lib"), "-lhipblaslt"] + HIP_LINK, verbose))
+    return {"kernels": KERNELS_OUT, "core": CORE_OUT, "config": CONFIG_OUT, "matmul": MATMUL_OUT}
 
 
 if __name__ == "__main__":

@@ -1,7 +1,7 @@
 /*
  * Op API: build an Op on the stack (skeleton + pointers to each argument, in
  * skeleton order) and submit it. Argument order and meaning follow the
- * reference's src/dataflow_ops/src/{preprocess_ops.c:3-32, norm_ops.c:4-97,
+ * reference's src/dataflow_ops/src/{matmul_op.c:10-65, preprocess_ops.c:3-32, norm_ops.c:4-97,
  * attn_misc_ops.c:3-100, mlp_misc_ops.c:3-61, loss_misc_ops.c:4-60}.
  */
 #include "dataflow_ops.h"
@@ -16,6 +16,29 @@ static int submit_built_op(Dataflow_Handle * handle, Op * op, int stream_id, con
 		return -1;
 	}
 	return 0;
+}
+
+int submit_matmul(Dataflow_Handle * handle, int stream_id,
+					DataflowDatatype a_dt, DataflowDatatype b_dt, DataflowDatatype c_dt, DataflowDatatype d_dt,
+					DataflowDatatype compute_dt,
+					int to_trans_a, int to_trans_b,
+					int M, int K, int N,
+					float alpha, float beta,
+					void * A, void * B, void * C, void * D,
+					uint64_t workspaceBytes, void * workspace) {
+	Op op;
+	set_external_matmul_skeleton(&op.op_skeleton);
+	/* 0 = use every CU */
+	int num_procs = 0;
+	void ** a = op.op_args;
+	a[0] = &num_procs;
+	a[1] = &a_dt; a[2] = &b_dt; a[3] = &c_dt; a[4] = &d_dt; a[5] = &compute_dt;
+	a[6] = &to_trans_a; a[7] = &to_trans_b;
+	a[8] = &M; a[9] = &K; a[10] = &N;
+	a[11] = &alpha; a[12] = &beta;
+	a[13] = &A; a[14] = &B; a[15] = &C; a[16] = &D;
+	a[17] = &workspaceBytes; a[18] = &workspace;
+	return submit_built_op(handle, &op, stream_id, "matmul");
 }
 
 int submit_embedding(Dataflow_Handle * handle, int stream_id,

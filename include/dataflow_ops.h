@@ -2,8 +2,9 @@
  * Op API: each submit_* fills an Op (skeleton + pointers to its arguments)
  * and hands it to handle->submit_op. Returns 0, or -1 with a message on
  * stderr. Argument order and meaning follow the reference's
- * src/dataflow_ops/include/dataflow_ops.h:146-215. The external-library ops
- * of the reference (matmul, attention) are not part of this library.
+ * src/dataflow_ops/include/dataflow_ops.h:146-215. Of the reference's
+ * external-library ops, matmul is provided (through hipBLASLt); attention is
+ * not part of this library.
  */
 #ifndef DATAFLOW_OPS_H
 #define DATAFLOW_OPS_H
@@ -12,10 +13,29 @@
 #include "ops.h"
 #include "dataflow_handle.h"
 #include "set_native_op_skeletons.h"
+#include "set_external_op_skeletons.h"
 
 #ifdef __cplusplus
 extern "C" {
 #endif
+
+/* --- matmul (reference: src/dataflow_ops/src/matmul_op.c:10-65, external op) --- */
+
+/* BLAS column-major semantics: D [M x N] = alpha * op(A) * op(B) + beta * C,
+ * op(A) [M x K], op(B) [K x N]; A is stored M x K (ld M), or K x M (ld K)
+ * when to_trans_a; B is stored K x N (ld K), or N x K (ld N) when to_trans_b;
+ * C and D are M x N (ld M). With C == NULL, c_dt == DATAFLOW_NONE or
+ * beta == 0, C is not read. A row-major Y [m x n] = X [m x k] @ W, W stored
+ * column-major, is A = W, B = X, D = Y, to_trans_a = 1, M = n, K = k, N = m.
+ * Needs the matmul op registered (register_external_matmul). */
+int submit_matmul(Dataflow_Handle * handle, int stream_id,
+					DataflowDatatype a_dt, DataflowDatatype b_dt, DataflowDatatype c_dt, DataflowDatatype d_dt,
+					DataflowDatatype compute_dt,
+					int to_trans_a, int to_trans_b,
+					int M, int K, int N,
+					float alpha, float beta,
+					void * A, void * B, void * C, void * D,
+					uint64_t workspaceBytes, void * workspace);
 
 /* --- preprocess (reference: src/dataflow_ops/src/preprocess_ops.c:3-32) --- */
 

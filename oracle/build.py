@@ -25,6 +25,7 @@ REF_SOURCES = [
     "src/datatype/src/dataflow_datatype.c",
     "src/fingerprint/src/fingerprint.c",
     "src/set_ops/src/set_native_op_skeletons.c",
+    "src/set_ops/src/set_external_op_skeletons.c",
     "src/table/src/table.c",
 ]
 # exported registry-path entry points; everything else is local and
@@ -37,7 +38,7 @@ REF_EXPORTS = [
     "set_native_rms_norm_bwd_x_skeleton", "set_native_rms_norm_bwd_w_skeleton", "set_native_rope_skeleton",
     "set_native_rope_bwd_x_skeleton", "set_native_copy_to_seq_context_skeleton", "set_native_swiglu_skeleton",
     "set_native_swiglu_bwd_x_skeleton", "set_native_softmax_skeleton", "set_native_cross_entropy_loss_skeleton",
-    "register_native_ops", "init_table", "insert_table", "find_table", "remove_table", "destroy_table",
+    "register_native_ops", "set_external_matmul_skeleton", "init_table", "insert_table", "find_table", "remove_table", "destroy_table",
 ]
 REF_INCLUDES = [
     "include", "src/datatype/include", "src/fingerprint/include", "src/ops/include",

@@ -51,8 +51,8 @@ def test_every_declared_symbol_is_exported():
 def test_parser_sees_the_op_api():
     names = declared_functions(os.path.join(INCLUDE, "dataflow_ops.h"))
     assert {"submit_rms_norm", "submit_rope_bwd_x", "submit_softmax_cross_entropy_loss", "submit_embedding",
-            "submit_copy_to_seq_context"} <= set(names)
-    assert len(names) == 13
+            "submit_copy_to_seq_context", "submit_matmul"} <= set(names)
+    assert len(names) == 14
 
 
 def test_kernel_code_object_present():

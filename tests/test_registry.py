@@ -227,3 +227,18 @@ def test_table_slot_indices_match_reference_build():
         mine = run_ops(api.lib(), 100 + seed, size_max=512)
         theirs = run_ops(L, 100 + seed, size_max=512)
         assert mine == theirs
+
+
+def test_external_matmul_skeleton_matches_reference_build():
+    """the matmul skeleton (19 args) is byte-identical to the reference's, so
+    an Op built by either side resolves to the same table entry"""
+    L = ref_lib()
+    L.set_external_matmul_skeleton.argtypes = [ctypes.POINTER(api.OpSkeleton)]
+    api.lib().set_external_matmul_skeleton.argtypes = [ctypes.POINTER(api.OpSkeleton)]
+    mine, ref = api.OpSkeleton(), api.OpSkeleton()
+    api.lib().set_external_matmul_skeleton(ctypes.byref(mine))
+    L.set_external_matmul_skeleton(ctypes.byref(ref))
+    assert bytes(mine) == bytes(ref)
+    assert mine.header.op_nickname.decode() == "matmul" and mine.header.num_args == 19
+    digest = hashlib.sha256(bytes(mine.header)).digest()
+    assert bytes(mine.fingerprint)[:32] == digest
