@@ -20,7 +20,9 @@ bytes / measured step time. Timed as extras, outside `value`: the
 reference-compatible split ops (rms_norm_bwd_x, rms_norm_bwd_w, softmax,
 cross_entropy_loss) and the path's neighbours (embedding gather of 8192 rows
 of a 128256 x 4096 bf16 table; copy_to_seq_context of K, V [8192 x 1024] bf16
-into 4 contexts of 2048 positions).
+into 4 contexts of 2048 positions). `transformer_head`: the loss-path driver
+(submit_transformer_head, training pass) at 4096 tokens x 4096 x 128256, whose
+time is its three hipBLASLt GEMMs (reported in TFLOP/s).
 
 cpu_baseline: the C oracle (oracle/liboracle.so, OpenMP over rows, fp64
 arithmetic) on a bounded row sample of the same ops, timed on this host.
@@ -278,6 +280,40 @@ def time_ops(h, hip, ops, steps, warmup):
     return per_op, step_ms, wall
 
 
+def time_head(h, hip, pool, api, iters):
+    """submit_transformer_head, training pass (norm, output projection, fused
+    loss, both backward GEMMs, norm backward) at 4096 tokens x 4096 x 128256
+    bf16; reported beside the path, not in `value`: its time is the three
+    hipBLASLt GEMMs' (6 * T * E * V flop)."""
+    T, E, V = 4096, 4096, 128256
+    X, wn = pool.fill(T * E * 2, "normal_bf16", 40), pool.fill(E * 2, "normal_bf16", 41, 1.0, 0.02)
+    W, dW = pool.fill(V * E * 2, "normal_bf16", 42, 0.0, E ** -0.5), pool.fill(V * E * 2, "zeros")
+    dwn, dX = pool.fill(E * 4, "zeros"), pool.fill(T * E * 2, "zeros")
+    labels = pool.put(np.random.default_rng(43).integers(0, V, size=T).astype(np.uint32))
+    norm, wsum, rs, out = pool.empty(T * E * 2), pool.empty(T * 4), pool.empty(T * 4), pool.empty(T * V * 2)
+    loss, gnorm, ws = pool.empty((T + 1) * 4), pool.empty(T * E * 2), pool.empty(32 << 20)
+    head = api.TransformerHead(BF16, BF16, 3, 1e-5, api.EmbeddingConfig(V, E), None, wn, W)
+    acts = api.TransformerHeadActivations(T, None, norm, wsum, rs, out, ws, 32 << 20)
+    ghead = api.TransformerHead(BF16, BF16, 3, 1e-5, api.EmbeddingConfig(V, E), None, dwn, dW)
+    gacts = api.TransformerHeadActivations(T, None, gnorm, None, None, None, ws, 32 << 20)
+    inp, gstream = api.TransformerBlockTransition(None, X), api.TransformerBlockTransition(None, dX)
+    mo = api.TransformerModelOutput(None, None, labels, None, loss, 0.0)
+    run = lambda: api.submit_transformer_head(h, 0, 0, inp, head, acts, mo, ghead, gacts, gstream, None)
+    for _ in range(2):
+        assert run() == 0
+    h.sync()
+    stream = h.stream(0)
+    a, b = hip.event(), hip.event()
+    hip.record(a, stream)
+    for _ in range(iters):
+        assert run() == 0
+    hip.record(b, stream)
+    ms = hip.elapsed_ms(a, b) / iters
+    flop = 6.0 * T * E * V
+    return {"ms": round(ms, 3), "matmul_tflops": round(flop / (ms * 1e-3) / 1e12, 1), "tokens": T, "embedding": E,
+            "vocab": V, "iters": iters, "note": "submit_transformer_head training pass; GEMMs on hipBLASLt"}
+
+
 def cpu_baseline(budget_s):
     """Oracle (C, fp64, OpenMP over rows) on a row sample of the same ops."""
     sys.path.insert(0, os.path.join(ROOT, "tests"))
@@ -352,6 +388,7 @@ def main():
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=3)
     ap.add_argument("--no-extras", action="store_true")
+    ap.add_argument("--no-head", action="store_true", help="skip the transformer-head (GEMM) line")
     ap.add_argument("--cpu-budget", type=float, default=15.0, help="seconds of CPU baseline work")
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--copy-calibration", action="store_true",
@@ -365,7 +402,7 @@ def main():
         sys.exit(2)
     from dataflow_lib_amd import api
     hip = Hip()
-    h = api.Handle(0, num_streams=1)
+    h = api.Handle(0, num_streams=1, matmul=not args.no_head)
     pool = Pool(h)
     try:
         print("bench: allocating and filling rotating buffer sets", file=sys.stderr, flush=True)
@@ -375,6 +412,7 @@ def main():
         print("bench: timing %d steps after %d warmup" % (args.steps, args.warmup), file=sys.stderr, flush=True)
         per_op, step_ms, wall = time_ops(h, hip, ops, args.steps, args.warmup)
         per_extra = time_ops(h, hip, extras, max(5, args.steps // 2), 1)[0] if extras else {}
+        head = None if args.no_head else time_head(h, hip, pool, api, 5)
         if args.copy_calibration:
             src, dst = pool.empty(GiB), pool.empty(GiB)
             for _ in range(4):
@@ -405,7 +443,8 @@ def main():
                                "swiglu fwd+bwd 8192x14336, fused softmax+xent 4096x128256",
                    "tokens": 8192, "hidden": 4096, "ffn": 14336, "vocab": 128256, "ce_rows": 4096},
         "pct_of_peak": round(100.0 * value / HBM_PEAK_GBPS, 1),
-        "ops": per_op, "extras": per_extra, "roofline": roofline, "cpu_baseline": cpu, "device": dev,
+        "ops": per_op, "extras": per_extra, "transformer_head": head, "roofline": roofline, "cpu_baseline": cpu,
+        "device": dev,
         "wall_s_timed": round(wall, 3),
     }
     print(json.dumps(line))
