@@ -41,9 +41,9 @@
 /* embedding / copy_to_seq_context: one wave per row, 4 waves per workgroup */
 #define GS_WAVES 4
 
-/* SwiGLU: grid-stride, one 512-thread workgroup per CU, 16-byte chunks per
- * thread in flight */
-#define SWIGLU_UNROLL 4
+/* SwiGLU: grid-stride, one 512-thread workgroup per CU; per thread and
+ * stream, 2 16-byte chunks computed per step while the next 2 load */
+#define SWIGLU_UNROLL 2
 #define SWIGLU_THREADS 512
 #define SWIGLU_WG_PER_CU 1
 

@@ -11,10 +11,13 @@
  * finite where the reference's form gives inf - inf = NaN (g < -88.7).
  *
  * Pure streaming: the [rows x cols] tensors are treated as flat arrays,
- * grid-stride over 16-byte chunks, four chunks per thread in flight, with
- * non-temporal loads and stores. The launch uses one large workgroup per CU
- * so that at any moment the whole GPU sweeps one compact window of memory,
- * which is where gfx950's HBM sustains its highest mixed read/write rate.
+ * grid-stride over 16-byte chunks, SWIGLU_UNROLL chunks per thread and
+ * stream per step, software-pipelined: the next step's loads are issued
+ * before this step's chunks are computed and stored, so every wave keeps
+ * loads in flight through its arithmetic. Loads and stores are
+ * non-temporal. The launch uses one large workgroup per CU so that at any
+ * moment the whole GPU sweeps one compact window of memory, which is where
+ * gfx950's HBM sustains its highest mixed read/write rate.
  */
 #include "dtypes.h"
 #include "kernel_geometry.h"
@@ -53,12 +56,18 @@ __device__ __forceinline__ void swiglu_fwd(long n, const T * g, const T * u, T *
 	const R16 * uv = reinterpret_cast<const R16 *>(u);
 	R16 * ov = reinterpret_cast<R16 *>(out);
 
+	R16 gr[SWIGLU_UNROLL], ur[SWIGLU_UNROLL];
+#pragma unroll
+	for (int k = 0; k < SWIGLU_UNROLL; k++) {
+		const long v = tid + k * nth;
+		if (v < nvec) { gr[k] = ld16_nt(gv + v); ur[k] = ld16_nt(uv + v); }
+	}
 	for (long v0 = tid; v0 < nvec; v0 += nth * SWIGLU_UNROLL) {
-		R16 gr[SWIGLU_UNROLL], ur[SWIGLU_UNROLL];
+		R16 gn[SWIGLU_UNROLL], un[SWIGLU_UNROLL];
 #pragma unroll
 		for (int k = 0; k < SWIGLU_UNROLL; k++) {
-			const long v = v0 + k * nth;
-			if (v < nvec) { gr[k] = ld16_nt(gv + v); ur[k] = ld16_nt(uv + v); }
+			const long v = v0 + (SWIGLU_UNROLL + k) * nth;
+			if (v < nvec) { gn[k] = ld16_nt(gv + v); un[k] = ld16_nt(uv + v); }
 		}
 #pragma unroll
 		for (int k = 0; k < SWIGLU_UNROLL; k++) {
@@ -72,6 +81,8 @@ __device__ __forceinline__ void swiglu_fwd(long n, const T * g, const T * u, T *
 				st16_nt(ov + v, pack16<T>(of));
 			}
 		}
+#pragma unroll
+		for (int k = 0; k < SWIGLU_UNROLL; k++) { gr[k] = gn[k]; ur[k] = un[k]; }
 	}
 	for (long i = nvec * VEC + tid; i < n; i += nth) {
 		out[i] = from_f<T>(swiglu_fwd_elem(to_f(g[i]), to_f(u[i])));
@@ -105,12 +116,18 @@ __device__ __forceinline__ void swiglu_bwd(long n, const T * g, const T * u, con
 	R16 * dgv = reinterpret_cast<R16 *>(dG);
 	R16 * duv = reinterpret_cast<R16 *>(dU);
 
+	R16 gr[SWIGLU_UNROLL], ur[SWIGLU_UNROLL], dr[SWIGLU_UNROLL];
+#pragma unroll
+	for (int k = 0; k < SWIGLU_UNROLL; k++) {
+		const long v = tid + k * nth;
+		if (v < nvec) { gr[k] = ld16_nt(gv + v); ur[k] = ld16_nt(uv + v); dr[k] = ld16_nt(dv + v); }
+	}
 	for (long v0 = tid; v0 < nvec; v0 += nth * SWIGLU_UNROLL) {
-		R16 gr[SWIGLU_UNROLL], ur[SWIGLU_UNROLL], dr[SWIGLU_UNROLL];
+		R16 gn[SWIGLU_UNROLL], un[SWIGLU_UNROLL], dn[SWIGLU_UNROLL];
 #pragma unroll
 		for (int k = 0; k < SWIGLU_UNROLL; k++) {
-			const long v = v0 + k * nth;
-			if (v < nvec) { gr[k] = ld16_nt(gv + v); ur[k] = ld16_nt(uv + v); dr[k] = ld16_nt(dv + v); }
+			const long v = v0 + (SWIGLU_UNROLL + k) * nth;
+			if (v < nvec) { gn[k] = ld16_nt(gv + v); un[k] = ld16_nt(uv + v); dn[k] = ld16_nt(dv + v); }
 		}
 #pragma unroll
 		for (int k = 0; k < SWIGLU_UNROLL; k++) {
@@ -126,6 +143,8 @@ __device__ __forceinline__ void swiglu_bwd(long n, const T * g, const T * u, con
 				st16_nt(duv + v, pack16<T>(ouf));
 			}
 		}
+#pragma unroll
+		for (int k = 0; k < SWIGLU_UNROLL; k++) { gr[k] = gn[k]; ur[k] = un[k]; dr[k] = dn[k]; }
 	}
 	for (long i = nvec * VEC + tid; i < n; i += nth) {
 		float dg, du;
