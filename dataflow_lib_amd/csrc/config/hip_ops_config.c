@@ -172,7 +172,7 @@ int rms_norm_bwd_set_finish_launch_config(Hip_Launch_Config * hip_launch_config,
 
 /* ---------------- RoPE ---------------- */
 
-static int rope_config(Hip_Launch_Config * c, Dataflow_Handle * h, Op * op, const char * what) {
+static int rope_config(Hip_Launch_Config * c, Dataflow_Handle * h, Hip_Function * f, Op * op, const char * what) {
 	const uint64_t N = ARG(op, 0, uint64_t);
 	const int model_dim = ARG(op, 1, int), head_dim = ARG(op, 2, int), num_kv_heads = ARG(op, 3, int);
 	if (model_dim <= 0 || head_dim <= 0 || (head_dim & 1) || head_dim > ROPE_MAX_HEAD_DIM || (model_dim % head_dim) != 0 ||
@@ -183,21 +183,28 @@ static int rope_config(Hip_Launch_Config * c, Dataflow_Handle * h, Op * op, cons
 		return -1;
 	}
 	const uint64_t n_tokens = N / (uint64_t) model_dim;
-	/* one wave per token, looping; four workgroups per CU measured best */
-	uint64_t grid = MY_CEIL(n_tokens, (uint64_t) ROPE_WAVES);
+	const size_t elem = arg_elem_bytes(f, 6);
+	const unsigned long long ptr_or = ptr_bits(ARG(op, 6, void *)) | ptr_bits(ARG(op, 7, void *));
+	uint64_t grid;
+	if (elem != 0 && rope_slot_ok(model_dim, num_kv_heads * head_dim, head_dim, (int) elem, ptr_or)) {
+		/* vector path: one workgroup per token at a time, persistent */
+		grid = MY_MIN(n_tokens, (uint64_t) dev(h)->cu_count * ROPE_SLOT_WG_PER_CU);
+		set_1d(c, (unsigned) grid, ROPE_SLOT_THREADS, 0);
+		return 0;
+	}
+	/* element path: one wave per token, looping; four workgroups per CU */
+	grid = MY_CEIL(n_tokens, (uint64_t) ROPE_WAVES);
 	grid = MY_MIN(grid, (uint64_t) dev(h)->cu_count * 4u);
 	set_1d(c, (unsigned) grid, 64 * ROPE_WAVES, 0);
 	return 0;
 }
 
 int rope_set_launch_config(Hip_Launch_Config * hip_launch_config, Dataflow_Handle * dataflow_handle, Hip_Function * hip_function, Op * op) {
-	(void) hip_function;
-	return rope_config(hip_launch_config, dataflow_handle, op, "rope");
+	return rope_config(hip_launch_config, dataflow_handle, hip_function, op, "rope");
 }
 
 int rope_bwd_x_set_launch_config(Hip_Launch_Config * hip_launch_config, Dataflow_Handle * dataflow_handle, Hip_Function * hip_function, Op * op) {
-	(void) hip_function;
-	return rope_config(hip_launch_config, dataflow_handle, op, "rope bwd x");
+	return rope_config(hip_launch_config, dataflow_handle, hip_function, op, "rope bwd x");
 }
 
 /* ---------------- embedding / copy_to_seq_context ---------------- */

@@ -34,9 +34,18 @@
  * other SMX_MAXCH - SMX_PF chunks of the next row are prefetched into VGPRs */
 #define SMX_PF 9
 
-/* RoPE: one wave per token, 4 waves per workgroup, head_dim <= 512 */
+/* RoPE, head_dim <= 512. Vector path: one ROPE_SLOT_THREADS workgroup per
+ * token at a time (persistent over tokens, next token prefetched), thread t
+ * owning Q chunks t + 256 j (j < ROPE_QJ) and K chunks t + 256 j (j < ROPE_KJ)
+ * of 16 bytes. Element path (unaligned rows or head_dim not a multiple of the
+ * vector): one wave per token, ROPE_WAVES waves per workgroup. */
 #define ROPE_MAX_HEAD_DIM 512
 #define ROPE_WAVES 4
+#define ROPE_SLOT_THREADS 256
+#define ROPE_QJ 4
+#define ROPE_KJ 2
+/* vector path workgroups per CU (its register use allows four) */
+#define ROPE_SLOT_WG_PER_CU 4
 
 /* embedding / copy_to_seq_context: one wave per row, 4 waves per workgroup */
 #define GS_WAVES 4
@@ -66,6 +75,13 @@ GEOM_FN int rms_tpr_for(int nv) {
 	if (nv == 0) return RMS_STREAM_TPR;
 	const int t = (nv + RMS_CH - 1) / RMS_CH;
 	return ((t + 63) / 64) * 64;
+}
+
+/* RoPE: whether the vector (slot) path applies */
+GEOM_FN int rope_slot_ok(int model_dim, int kv_dim, int head_dim, int elem_bytes, unsigned long long ptr_or) {
+	const int vec = 16 / elem_bytes;
+	if ((head_dim % vec) != 0 || (ptr_or & 15ull) != 0ull) return 0;
+	return (model_dim / vec) <= ROPE_SLOT_THREADS * ROPE_QJ && (kv_dim / vec) <= ROPE_SLOT_THREADS * ROPE_KJ;
 }
 
 #endif

@@ -135,14 +135,138 @@ __device__ __forceinline__ void rope_impl(uint64_t N, int model_dim, int head_di
 	}
 }
 
+/* pair index (column / 2) of 16-byte chunk `chunk` of a Q or K row */
+template <typename T>
+__device__ __forceinline__ int rope_pair_of(int chunk, int head_dim, bool pow2) {
+	constexpr int VEC = VecOf<T>::N;
+	const int col = pow2 ? ((chunk * VEC) & (head_dim - 1)) : ((chunk * VEC) % head_dim);
+	return col >> 1;
+}
+
+/* Vector path: one workgroup of ROPE_SLOT_THREADS per token at a time,
+ * persistent over tokens t = block, block + grid, ... The next token's Q and
+ * K chunks are loaded, and wave 0 builds its cos/sin table into the other
+ * half of a double-buffered LDS table, while this token is rotated and
+ * stored; one barrier per token. Rows are addressed through per-row buffer
+ * ranges (chunks past a row read zero and store nowhere). */
+template <typename T, bool BWD>
+__device__ __forceinline__ void rope_slot(long n_tokens, int model_dim, int head_dim, int kv_dim, int theta,
+											const int * seq_positions, T * X_q, T * X_k) {
+	constexpr int VEC = VecOf<T>::N;
+	constexpr int NT = ROPE_SLOT_THREADS;
+	__shared__ float ang[ROPE_MAX_HEAD_DIM / 2];
+	__shared__ __attribute__((aligned(16))) float2 tab[2][ROPE_MAX_HEAD_DIM / 2];
+	const int tid = threadIdx.x;
+	const int lane = tid & 63;
+	const bool wave0 = __builtin_amdgcn_readfirstlane(tid >> 6) == 0;
+	const int half = head_dim >> 1;
+	/* angle_p, exactly as the reference's fp32 expression
+	 * powf(theta, -((float) c / (float) head_dim)) evaluated correctly rounded */
+	for (int p = tid; p < half; p += NT) ang[p] = (float) pow((double) (float) theta, (double) -((float) (2 * p) / (float) head_dim));
+
+	const int nvq = model_dim / VEC, nvk = kv_dim / VEC;
+	const uint32_t qbytes = (uint32_t) model_dim * (uint32_t) sizeof(T), kbytes = (uint32_t) kv_dim * (uint32_t) sizeof(T);
+	const bool pow2 = (head_dim & (head_dim - 1)) == 0;
+	/* pair index of each owned chunk: the same in every Q and K row, since
+	 * both rows start at a head boundary */
+	int pr[ROPE_QJ];
+#pragma unroll
+	for (int j = 0; j < ROPE_QJ; j++) pr[j] = rope_pair_of<T>(tid + NT * j, head_dim, pow2);
+
+	/* the cos/sin table of token t into tab[b] (wave 0) */
+	auto table = [&](long t, int b) {
+		const float fpos = (float) seq_positions[t];
+		for (int p = lane; p < half; p += 64) {
+			const float arg = fpos * ang[p];
+			double sd, cd;
+			sincos((double) arg, &sd, &cd);
+			tab[b][p] = make_float2((float) cd, (float) sd);
+		}
+	};
+	auto load = [&](long t, R16 (&q)[ROPE_QJ], R16 (&k)[ROPE_KJ]) {
+		const __amdgpu_buffer_rsrc_t rq = make_rsrc(X_q + t * model_dim, qbytes);
+		const __amdgpu_buffer_rsrc_t rk = make_rsrc(X_k + t * kv_dim, kbytes);
+#pragma unroll
+		for (int j = 0; j < ROPE_QJ; j++)
+			if (NT * j < nvq) q[j] = buf_load16_nt(rq, (uint32_t) (tid + NT * j) * 16u, 0);
+#pragma unroll
+		for (int j = 0; j < ROPE_KJ; j++)
+			if (NT * j < nvk) k[j] = buf_load16_nt(rk, (uint32_t) (tid + NT * j) * 16u, 0);
+	};
+	auto rot = [&](R16 & r, int p0, const float2 * cs) {
+		float f[VEC];
+		unpack16<T>(r, f);
+#pragma unroll
+		for (int q = 0; q < VEC / 2; q++) {
+			const float2 c = cs[p0 + q];
+			rotate<BWD>(c.x, c.y, f[2 * q], f[2 * q + 1], f[2 * q], f[2 * q + 1]);
+		}
+		r = pack16<T>(f);
+	};
+
+	long t = blockIdx.x;
+	const long stride = gridDim.x;
+	__syncthreads();   /* angles */
+	R16 q[ROPE_QJ], k[ROPE_KJ];
+	if (t < n_tokens) {
+		load(t, q, k);
+		if (wave0) table(t, 0);
+	}
+	__syncthreads();
+	int b = 0;
+	for (; t < n_tokens; t += stride) {
+		const long tn = t + stride;
+		R16 qn[ROPE_QJ], kn[ROPE_KJ];
+		if (tn < n_tokens) {
+			load(tn, qn, kn);
+			if (wave0) table(tn, b ^ 1);
+		}
+		const float2 * cs = tab[b];
+		const __amdgpu_buffer_rsrc_t rq = make_rsrc(X_q + t * model_dim, qbytes);
+		const __amdgpu_buffer_rsrc_t rk = make_rsrc(X_k + t * kv_dim, kbytes);
+#pragma unroll
+		for (int j = 0; j < ROPE_QJ; j++) {
+			if (NT * j < nvq) {
+				rot(q[j], pr[j], cs);
+				buf_store16_nt(rq, (uint32_t) (tid + NT * j) * 16u, 0, q[j]);
+			}
+		}
+#pragma unroll
+		for (int j = 0; j < ROPE_KJ; j++) {
+			if (NT * j < nvk) {
+				rot(k[j], pr[j], cs);
+				buf_store16_nt(rk, (uint32_t) (tid + NT * j) * 16u, 0, k[j]);
+			}
+		}
+		/* tab[b ^ 1] complete, and every read of tab[b] done before it is rebuilt */
+		__syncthreads();
+#pragma unroll
+		for (int j = 0; j < ROPE_QJ; j++) q[j] = qn[j];
+#pragma unroll
+		for (int j = 0; j < ROPE_KJ; j++) k[j] = kn[j];
+		b ^= 1;
+	}
+}
+
+template <typename T, bool BWD>
+__device__ __forceinline__ void rope_dispatch(uint64_t N, int model_dim, int head_dim, int num_kv_heads, int theta,
+											const int * seq_positions, T * X_q, T * X_k) {
+	const int kv_dim = num_kv_heads * head_dim;
+	const unsigned long long ptr_or = (unsigned long long) (uintptr_t) X_q | (unsigned long long) (uintptr_t) X_k;
+	if (blockDim.x == ROPE_SLOT_THREADS && rope_slot_ok(model_dim, kv_dim, head_dim, (int) sizeof(T), ptr_or))
+		rope_slot<T, BWD>((long) (N / (uint64_t) model_dim), model_dim, head_dim, kv_dim, theta, seq_positions, X_q, X_k);
+	else
+		rope_impl<T, BWD>(N, model_dim, head_dim, num_kv_heads, theta, seq_positions, X_q, X_k);
+}
+
 #define ROPE_KERNELS(SUFFIX, T)                                                                                     \
 	extern "C" __global__ void __launch_bounds__(256) rope_##SUFFIX##_kernel(uint64_t N, int model_dim, int head_dim, \
 			int num_kv_heads, int theta, int * seq_positions, T * X_q, T * X_k) {                                    \
-		rope_impl<T, false>(N, model_dim, head_dim, num_kv_heads, theta, seq_positions, X_q, X_k);                  \
+		rope_dispatch<T, false>(N, model_dim, head_dim, num_kv_heads, theta, seq_positions, X_q, X_k);              \
 	}                                                                                                               \
 	extern "C" __global__ void __launch_bounds__(256) rope_bwd_x_##SUFFIX##_kernel(uint64_t N, int model_dim, int head_dim, \
 			int num_kv_heads, int theta, int * seq_positions, T * dX_q, T * dX_k) {                                  \
-		rope_impl<T, true>(N, model_dim, head_dim, num_kv_heads, theta, seq_positions, dX_q, dX_k);                 \
+		rope_dispatch<T, true>(N, model_dim, head_dim, num_kv_heads, theta, seq_positions, dX_q, dX_k);             \
 	}
 
 ROPE_KERNELS(fp32, float)
