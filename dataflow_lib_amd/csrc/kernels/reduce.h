@@ -10,6 +10,19 @@
 
 #include <hip/hip_runtime.h>
 
+/* Workgroup barrier that orders LDS only. __syncthreads() is a release/acquire
+ * fence over all memory, so every wave first waits for all of its outstanding
+ * global loads and stores (vmcnt 0), which stalls loads issued early for later
+ * work. This barrier waits only for the wave's own LDS accesses (lgkmcnt 0), so
+ * such loads stay in flight across it. Use it only where the barrier publishes
+ * LDS data (direct-to-LDS buffer loads are vector-memory traffic and are not
+ * covered). */
+__device__ __forceinline__ void lds_barrier() {
+	__builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
+	__builtin_amdgcn_s_barrier();
+	__builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
+}
+
 template <int CTRL>
 __device__ __forceinline__ float dpp_f32(float v) {
 	return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), CTRL, 0xf, 0xf, false));
@@ -50,7 +63,7 @@ __device__ __forceinline__ float wave_max(float v) {
 template <int NW>
 __device__ __forceinline__ float group_sum(float wave_total, float * slots, int wave_in_group) {
 	if ((threadIdx.x & 63) == 0) slots[wave_in_group] = wave_total;
-	__syncthreads();
+	lds_barrier();
 	float t = 0.0f;
 #pragma unroll
 	for (int w = 0; w < NW; w++) t += slots[w];

@@ -64,7 +64,7 @@ __device__ __forceinline__ void slot_sum2(float & a, float & b, float * cells, i
 	b = wave_sum(b);
 	float * c = cells + (parity * slots + slot) * 32;
 	if ((threadIdx.x & 63) == 0) { c[wave_in_slot] = a; c[16 + wave_in_slot] = b; }
-	__syncthreads();
+	lds_barrier();
 	float ta = 0.0f, tb = 0.0f;
 	for (int w = 0; w < waves_per_slot; w++) { ta += c[w]; tb += c[16 + w]; }
 	a = ta;

@@ -16,6 +16,7 @@
  * the fp32 result is within ~1 ulp even when the two products cancel.
  */
 #include "dtypes.h"
+#include "reduce.h"
 #include "kernel_geometry.h"
 
 /* a*b + c*d, with the rounding error of c*d added back */
@@ -37,10 +38,12 @@ __device__ __forceinline__ void rotate(float c, float s, float e, float o, float
 	}
 }
 
+/* orders this wave's LDS table writes and reads (LDS only, so the wave's
+ * global loads and stores stay in flight) */
 __device__ __forceinline__ void wave_lds_sync() {
-	__builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
+	__builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
 	__builtin_amdgcn_wave_barrier();
-	__builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup");
+	__builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
 }
 
 /* rotate one row (Q or K) of `width` elements with the token's table */
@@ -206,13 +209,13 @@ __device__ __forceinline__ void rope_slot(long n_tokens, int model_dim, int head
 
 	long t = blockIdx.x;
 	const long stride = gridDim.x;
-	__syncthreads();   /* angles */
+	lds_barrier();   /* angles */
 	R16 q[ROPE_QJ], k[ROPE_KJ];
 	if (t < n_tokens) {
 		load(t, q, k);
 		if (wave0) table(t, 0);
 	}
-	__syncthreads();
+	lds_barrier();
 	int b = 0;
 	for (; t < n_tokens; t += stride) {
 		const long tn = t + stride;
@@ -238,8 +241,9 @@ __device__ __forceinline__ void rope_slot(long n_tokens, int model_dim, int head
 				buf_store16_nt(rk, (uint32_t) (tid + NT * j) * 16u, 0, k[j]);
 			}
 		}
-		/* tab[b ^ 1] complete, and every read of tab[b] done before it is rebuilt */
-		__syncthreads();
+		/* tab[b ^ 1] complete, and every read of tab[b] done before it is
+		 * rebuilt; the next token's loads stay in flight across it */
+		lds_barrier();
 #pragma unroll
 		for (int j = 0; j < ROPE_QJ; j++) q[j] = qn[j];
 #pragma unroll

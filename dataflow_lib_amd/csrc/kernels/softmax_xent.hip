@@ -41,7 +41,7 @@ __device__ __forceinline__ float block_max(float v, float * slots) {
 	v = wave_max(v);
 	const int nw = blockDim.x >> 6;
 	if ((threadIdx.x & 63) == 0) slots[threadIdx.x >> 6] = v;
-	__syncthreads();
+	lds_barrier();
 	float m = slots[0];
 	for (int w = 1; w < nw; w++) m = fmaxf(m, slots[w]);
 	return m;
@@ -52,9 +52,62 @@ __device__ __forceinline__ void block_sum2(float & a, float & b, float * slots) 
 	b = wave_sum(b);
 	const int nw = blockDim.x >> 6;
 	if ((threadIdx.x & 63) == 0) { slots[threadIdx.x >> 6] = a; slots[16 + (threadIdx.x >> 6)] = b; }
-	__syncthreads();
+	lds_barrier();
 	float sa = 0.0f, sb = 0.0f;
 	for (int w = 0; w < nw; w++) { sa += slots[w]; sb += slots[16 + w]; }
+	a = sa;
+	b = sb;
+}
+
+/* Reductions of the register-row path, which keeps direct-to-LDS loads of
+ * the next row in flight across them. The compiler cannot tell that those
+ * loads write other LDS cells than the reduction's, so a fenced barrier or a
+ * plain LDS read after it would first wait for every outstanding vector-memory
+ * access (vmcnt 0), stalling on the prefetch. Here each wave's partial is
+ * published with an explicit LDS wait + s_barrier and the cells are read back
+ * with ds_read_b128 issued from inline assembly (each followed by its own
+ * lgkmcnt wait), so only LDS traffic is waited for. The cells (16-byte
+ * aligned, one per wave of SMX_THREADS) never overlap the prefetch buffer. */
+typedef float f32x4_v __attribute__((ext_vector_type(4)));
+constexpr int SMX_WAVES = SMX_THREADS / 64;
+static_assert(SMX_WAVES % 4 == 0, "cells are read four at a time");
+
+__device__ __forceinline__ void cells_barrier() {
+	__asm__ volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+}
+__device__ __forceinline__ f32x4_v cells_read4(const float * cell) {
+	const uint32_t a = (uint32_t) (uintptr_t) (const __attribute__((address_space(3))) float *) cell;
+	f32x4_v v;
+	__asm__ volatile("ds_read_b128 %0, %1\n\ts_waitcnt lgkmcnt(0)" : "=v"(v) : "v"(a) : "memory");
+	return v;
+}
+/* same results, combined in the same wave order, as block_max / block_sum2 */
+__device__ __forceinline__ float cells_max(float v, float * cells) {
+	v = wave_max(v);
+	if ((threadIdx.x & 63) == 0) cells[threadIdx.x >> 6] = v;
+	cells_barrier();
+	float m = -__builtin_inff();
+#pragma unroll
+	for (int w = 0; w < SMX_WAVES; w += 4) {
+		const f32x4_v c = cells_read4(cells + w);
+		m = fmaxf(fmaxf(m, c.x), fmaxf(c.y, c.z));
+		m = fmaxf(m, c.w);
+	}
+	return m;
+}
+__device__ __forceinline__ void cells_sum2(float & a, float & b, float * cells) {
+	a = wave_sum(a);
+	b = wave_sum(b);
+	if ((threadIdx.x & 63) == 0) { cells[threadIdx.x >> 6] = a; cells[SMX_WAVES + (threadIdx.x >> 6)] = b; }
+	cells_barrier();
+	float sa = 0.0f, sb = 0.0f;
+#pragma unroll
+	for (int w = 0; w < SMX_WAVES; w += 4) {
+		const f32x4_v ca = cells_read4(cells + w);
+		const f32x4_v cb = cells_read4(cells + SMX_WAVES + w);
+		sa += ca.x; sa += ca.y; sa += ca.z; sa += ca.w;
+		sb += cb.x; sb += cb.y; sb += cb.z; sb += cb.w;
+	}
 	a = sa;
 	b = sb;
 }
@@ -84,6 +137,7 @@ __device__ __forceinline__ void mean_loss_finish(int n_rows, const float * loss,
 template <typename T> struct SmxWord;
 template <> struct SmxWord<bf16_t> {
 	static constexpr int N = 2;
+	static constexpr uint32_t NEG_INF = 0xff80ff80u;
 	__device__ static __forceinline__ void unpack(uint32_t w, float * f) { f[0] = bf16_lo(w); f[1] = bf16_hi(w); }
 	__device__ static __forceinline__ uint32_t pack(const float * f) { return pack_bf16x2(f[0], f[1]); }
 	__device__ static __forceinline__ uint32_t diff(uint32_t w, float m, float * x_m, float * d) {
@@ -99,6 +153,7 @@ template <> struct SmxWord<bf16_t> {
 };
 template <> struct SmxWord<f16_t> {
 	static constexpr int N = 2;
+	static constexpr uint32_t NEG_INF = 0xfc00fc00u;
 	__device__ static __forceinline__ void unpack(uint32_t w, float * f) {
 		const f16x2_v h = __builtin_bit_cast(f16x2_v, w);
 		f[0] = (float) h.x;
@@ -117,6 +172,7 @@ template <> struct SmxWord<f16_t> {
 };
 template <> struct SmxWord<float> {
 	static constexpr int N = 1;
+	static constexpr uint32_t NEG_INF = 0xff800000u;
 	__device__ static __forceinline__ void unpack(uint32_t w, float * f) { f[0] = __uint_as_float(w); }
 	__device__ static __forceinline__ uint32_t pack(const float * f) { return __float_as_uint(f[0]); }
 	__device__ static __forceinline__ uint32_t diff(uint32_t w, float m, float * x_m, float * d) {
@@ -149,12 +205,15 @@ typedef __attribute__((address_space(3))) void * lds_ptr_t;
 /* Register-resident row path, persistent over rows (row = block, block +
  * grid, ...). Chunk c of thread t is row chunk c * blockDim + t, addressed
  * through a per-row buffer resource (one VGPR offset for all chunks); the
- * whole row sits in VGPRs. The next row is fetched while this one computes:
- * its first SMX_PF chunks go straight into LDS (16-byte buffer loads with the
- * LDS bit) during the max and sum passes, and each of its other chunks is
- * loaded into chunk c's registers as soon as the output pass has stored this
- * row's chunk c. Each wave prefetches into and reads from its own LDS slice
- * only, so no workgroup barrier guards the buffer. */
+ * whole row sits in VGPRs. The next row is requested at the top of this one
+ * and lands while it computes: its first SMX_PF chunks go straight into LDS
+ * (16-byte buffer loads with the LDS bit), the others into registers, and the
+ * fused op's next label into an LDS cell (a 4-byte LDS load by wave 0; the
+ * word holding the labelled logit follows the same way once the label is
+ * known). Each wave prefetches into and reads from its own LDS slice only, so
+ * no workgroup barrier guards the buffer, and the reductions' barriers wait
+ * for LDS only: the one wait for memory in a row is the one before the output
+ * pass. */
 template <typename T, typename TO, bool FUSED>
 __device__ __forceinline__ void smx_regs(int n_rows, int n_cols, const T * X, TO * out, const uint32_t * labels, float * loss) {
 	constexpr int VEC = VecOf<T>::N;
@@ -166,17 +225,33 @@ __device__ __forceinline__ void smx_regs(int n_rows, int n_cols, const T * X, TO
 	/* separate LDS cells for the max and the sum: each is rewritten only after
 	 * every wave has passed the other reduction's barrier, so reuse needs no
 	 * barrier of its own (two barriers per row) */
-	__shared__ float mslots[16];
-	__shared__ float sslots[32];
+	__shared__ __attribute__((aligned(16))) float mslots[SMX_WAVES];
+	__shared__ __attribute__((aligned(16))) float sslots[2 * SMX_WAVES];
 	__shared__ __attribute__((aligned(16))) R16 pf[SMX_PF * SMX_THREADS];
+	__shared__ uint32_t labcell[64];          /* a row's label, one copy per lane of wave 0 */
+	__shared__ uint32_t xlabcell[64];         /* the 4-byte word holding its labelled logit */
 	const int tid = threadIdx.x;
 	constexpr int nt = SMX_THREADS;          /* the launch guarantees blockDim.x == SMX_THREADS */
+	static_assert((nt & (nt - 1)) == 0, "power-of-two workgroup");
 	constexpr uint32_t cstride = nt * 16u;   /* chunk stride: an immediate, rematerialised per use */
 	const int wave_base = tid & ~63;
 	const int nv = n_cols / VEC;
 	const int nch = (nv + nt - 1) / nt;
 	const uint32_t row_bytes = (uint32_t) n_cols * (uint32_t) sizeof(T);
 	const uint32_t voff = (uint32_t) tid * 16u;
+	const uint64_t lab_bytes = FUSED ? (uint64_t) n_rows * 4u : 0u;
+	const __amdgpu_buffer_rsrc_t rlab = make_rsrc(labels, (uint32_t) (lab_bytes < 0xffffffffull ? lab_bytes : 0xffffffffull));
+	auto fetch_label = [&](int r) {
+		if (FUSED && wave_base == 0)
+			__builtin_amdgcn_raw_ptr_buffer_load_lds(rlab, (lds_ptr_t) labcell, 4, 0u, (uint32_t) r * 4u, 0, 0);
+	};
+	/* the word of row r holding element j (rows are 16-byte aligned) */
+	auto fetch_logit_word = [&](int r, uint32_t j) {
+		if (FUSED && wave_base == 0) {
+			const __amdgpu_buffer_rsrc_t rr = make_rsrc(X + (long) r * n_cols, row_bytes);
+			__builtin_amdgcn_raw_ptr_buffer_load_lds(rr, (lds_ptr_t) xlabcell, 4, 0u, (j * (uint32_t) sizeof(T)) & ~3u, 0, 0);
+		}
+	};
 
 	/* chunks SMX_PF .. SMX_PF + RP - 1 of the next row are loaded a row ahead
 	 * into VGPRs; fp32 rows keep those registers for temporaries and load the
@@ -194,18 +269,14 @@ __device__ __forceinline__ void smx_regs(int n_rows, int n_cols, const T * X, TO
 #pragma unroll
 		for (int c = SMX_PF; c < SMX_PF + RP; c++)
 			if (c < nch) nx[c - SMX_PF] = buf_load16_nt(r0, voff, c * cstride);
+		fetch_label(row);
 	}
 	WAIT_VMEM_ALL();
 	for (; row < n_rows; row += gridDim.x) {
 		const __amdgpu_buffer_rsrc_t rout = make_rsrc(out + (long) row * n_cols, row_bytes);
-		uint32_t lab = 0xffffffffu;
-		float x_lab = 0.0f;
-		if (FUSED) {
-			lab = labels[row];
-			if (tid == 0 && lab < (uint32_t) n_cols) x_lab = to_f(X[(long) row * n_cols + lab]);
-		}
-		/* this row: the LDS part (landed: checked before the last output pass)
-		 * and the register part loaded during the last row */
+		/* this row: its label and the LDS part (landed: checked before the last
+		 * output pass) and the register part loaded during the last row */
+		const uint32_t lab = FUSED ? labcell[0] : 0xffffffffu;
 #pragma unroll
 		for (int c = 0; c < SMX_PF; c++)
 			if (c < nch) xr[c] = pf[c * nt + tid];
@@ -222,6 +293,10 @@ __device__ __forceinline__ void smx_regs(int n_rows, int n_cols, const T * X, TO
 		/* the whole next row is requested now and lands while this row computes */
 		const int next = row + gridDim.x;
 		const bool has_next = next < n_rows;
+		/* the labelled logit's word: landed by the wait before the output pass,
+		 * which is also before this row is overwritten */
+		const bool lab_ok = FUSED && lab < (uint32_t) n_cols;
+		if (lab_ok) fetch_logit_word(row, lab);
 		if (has_next) {
 			const __amdgpu_buffer_rsrc_t rn = make_rsrc(X + (long) next * n_cols, row_bytes);
 #pragma unroll
@@ -230,15 +305,32 @@ __device__ __forceinline__ void smx_regs(int n_rows, int n_cols, const T * X, TO
 #pragma unroll
 			for (int c = SMX_PF; c < SMX_PF + RP; c++)
 				if (c < nch) nx[c - SMX_PF] = buf_load16_nt(rn, voff, c * cstride);
+			fetch_label(next);
 		}
+
+		/* the label sits in chunk c_lab (workgroup-uniform) of thread t_lab,
+		 * element le */
+		/* the last chunk's lanes past the row end (zeros from the range check)
+		 * become -inf, which leaves the max, the sums and the correction
+		 * unchanged, so the passes below need no per-lane mask */
+#pragma unroll
+		for (int c = 0; c < SMX_MAXCH; c++) {
+			if (c == nch - 1 && c * nt + tid >= nv) {
+#pragma unroll
+				for (int i = 0; i < 4; i++) xr[c].w[i] = W::NEG_INF;
+			}
+		}
+
+		const int lab_chunk = lab_ok ? (int) (lab / VEC) : 0;
+		const int c_lab = lab_ok ? lab_chunk / nt : -1;
+		const int t_lab = lab_chunk & (nt - 1);
+		const int le = (int) (lab % VEC);
 
 		float m = -__builtin_inff();
 #pragma unroll
-		for (int c = 0; c < SMX_MAXCH; c++) {
-			/* chunks past the row end hold zeros: keep them out of the max */
-			if (c < nch && c * nt + tid < nv) m = chunk_max<T>(xr[c], m);
-		}
-		m = block_max(m, mslots);
+		for (int c = 0; c < SMX_MAXCH; c++)
+			if (c < nch) m = chunk_max<T>(xr[c], m);
+		m = cells_max(m, mslots);
 #pragma unroll
 		for (int c = 0; c < SMX_MAXCH; c++) reg_barrier(xr[c]);
 
@@ -249,7 +341,7 @@ __device__ __forceinline__ void smx_regs(int n_rows, int n_cols, const T * X, TO
 		float sd0 = 0.0f, sd1 = 0.0f, corr = 0.0f;
 #pragma unroll
 		for (int c = 0; c < SMX_MAXCH; c++) {
-			if (c < nch && c * nt + tid < nv) {
+			if (c < nch) {
 				R16 o;
 #pragma unroll
 				for (int i = 0; i < 4; i++) {
@@ -268,18 +360,15 @@ __device__ __forceinline__ void smx_regs(int n_rows, int n_cols, const T * X, TO
 		}
 		float sd = sd0 + sd1;
 		float sx = sd + corr;
-		block_sum2(sd, sx, sslots);
+		cells_sum2(sd, sx, sslots);
 		/* y = exp(d) / sd as one exp2: exp2(d * log2(e) - log2(sd)) */
 		const float nlog2s = -__builtin_amdgcn_logf(sd);
 		/* the next row's loads are the only vector-memory traffic in flight
 		 * here (issued a whole max and sum pass ago; this row's own loads were
-		 * consumed by the max pass); its LDS part must have landed before the
-		 * next row reads it */
+		 * consumed by the max pass); its LDS part and label must have landed
+		 * before the next row reads them */
 		WAIT_VMEM_ALL();
 
-		/* chunk and element holding the label (if any) */
-		const int lab_chunk = (lab < (uint32_t) n_cols) ? (int) (lab / VEC) : -1;
-		const int le = (int) (lab % VEC);
 #pragma unroll
 		for (int c = 0; c < SMX_MAXCH; c++) {
 			if (c < nch) {
@@ -292,17 +381,15 @@ __device__ __forceinline__ void smx_regs(int n_rows, int n_cols, const T * X, TO
 					for (int e = 0; e < W::N; e++) f[e] = __builtin_amdgcn_exp2f(fmaf(f[e], SMX_LOG2E, nlog2s));
 					o.w[i] = WO::pack(f);
 				}
-				/* the label's chunk: a wave-uniform branch taken by one wave per
-				 * row, so the other chunks carry no per-element label test */
-				const bool at_label = FUSED && (c * nt + tid) == lab_chunk;
-				if (FUSED && __builtin_amdgcn_ballot_w64(at_label) != 0ull) {
+				/* the label's chunk (a workgroup-uniform branch), in one thread */
+				if (FUSED && c == c_lab && tid == t_lab) {
 #pragma unroll
 					for (int i = 0; i < 4; i++) {
 						float f[W::N];
 						WO::unpack(o.w[i], f);
 #pragma unroll
 						for (int e = 0; e < W::N; e++)
-							if (at_label && i * W::N + e == le) f[e] -= 1.0f;
+							if (i * W::N + e == le) f[e] -= 1.0f;
 						o.w[i] = WO::pack(f);
 					}
 				}
@@ -310,7 +397,13 @@ __device__ __forceinline__ void smx_regs(int n_rows, int n_cols, const T * X, TO
 			}
 		}
 		if (FUSED && tid == 0 && loss) {
-			loss[row] = (lab < (uint32_t) n_cols) ? (logf(sx) + m - x_lab) : __builtin_nanf("");
+			float x_lab = 0.0f;
+			if (lab_ok) {
+				float f[W::N];
+				W::unpack(xlabcell[0], f);
+				x_lab = (W::N == 2 && (lab & 1)) ? f[W::N - 1] : f[0];
+			}
+			loss[row] = lab_ok ? (logf(sx) + m - x_lab) : __builtin_nanf("");
 		}
 	}
 	WAIT_VMEM_ALL();
