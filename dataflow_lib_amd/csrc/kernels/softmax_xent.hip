@@ -208,9 +208,9 @@ typedef __attribute__((address_space(3))) void * lds_ptr_t;
  * whole row sits in VGPRs. The next row is requested at the top of this one
  * and lands while it computes: its first SMX_PF chunks go straight into LDS
  * (16-byte buffer loads with the LDS bit), the others into registers, and the
- * fused op's next label into an LDS cell (a 4-byte LDS load by wave 0; the
- * word holding the labelled logit follows the same way once the label is
- * known). Each wave prefetches into and reads from its own LDS slice only, so
+ * fused op's next label into an LDS cell (a 4-byte LDS load per wave; the
+ * word holding the labelled logit follows the same way, for thread 0, once
+ * the label is known). Each wave prefetches into and reads from its own LDS slice only, so
  * no workgroup barrier guards the buffer, and the reductions' barriers wait
  * for LDS only: the one wait for memory in a row is the one before the output
  * pass. */
@@ -228,26 +228,34 @@ __device__ __forceinline__ void smx_regs(int n_rows, int n_cols, const T * X, TO
 	__shared__ __attribute__((aligned(16))) float mslots[SMX_WAVES];
 	__shared__ __attribute__((aligned(16))) float sslots[2 * SMX_WAVES];
 	__shared__ __attribute__((aligned(16))) R16 pf[SMX_PF * SMX_THREADS];
-	__shared__ uint32_t labcell[64];          /* a row's label, one copy per lane of wave 0 */
-	__shared__ uint32_t xlabcell[64];         /* the 4-byte word holding its labelled logit */
+	/* a row's label, one cell per wave: each wave loads its own copy, so its
+	 * own wait for memory covers it (a load issued by one wave is not waited
+	 * for by the others) */
+	__shared__ uint32_t labcell[SMX_WAVES];
+	__shared__ uint32_t xlabcell[1];          /* the 4-byte word holding the labelled logit (thread 0) */
 	const int tid = threadIdx.x;
 	constexpr int nt = SMX_THREADS;          /* the launch guarantees blockDim.x == SMX_THREADS */
 	static_assert((nt & (nt - 1)) == 0, "power-of-two workgroup");
 	constexpr uint32_t cstride = nt * 16u;   /* chunk stride: an immediate, rematerialised per use */
 	const int wave_base = tid & ~63;
+	const int lane = tid & 63;
+	const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
 	const int nv = n_cols / VEC;
 	const int nch = (nv + nt - 1) / nt;
 	const uint32_t row_bytes = (uint32_t) n_cols * (uint32_t) sizeof(T);
 	const uint32_t voff = (uint32_t) tid * 16u;
 	const uint64_t lab_bytes = FUSED ? (uint64_t) n_rows * 4u : 0u;
 	const __amdgpu_buffer_rsrc_t rlab = make_rsrc(labels, (uint32_t) (lab_bytes < 0xffffffffull ? lab_bytes : 0xffffffffull));
+	/* 4-byte loads straight into LDS from lane 0 only (lane l would write
+	 * the cell at 4 l) */
 	auto fetch_label = [&](int r) {
-		if (FUSED && wave_base == 0)
-			__builtin_amdgcn_raw_ptr_buffer_load_lds(rlab, (lds_ptr_t) labcell, 4, 0u, (uint32_t) r * 4u, 0, 0);
+		if (FUSED && lane == 0)
+			__builtin_amdgcn_raw_ptr_buffer_load_lds(rlab, (lds_ptr_t) &labcell[wave], 4, 0u, (uint32_t) r * 4u, 0, 0);
 	};
-	/* the word of row r holding element j (rows are 16-byte aligned) */
+	/* the word of row r holding element j (rows are 16-byte aligned), for
+	 * thread 0, which writes the loss */
 	auto fetch_logit_word = [&](int r, uint32_t j) {
-		if (FUSED && wave_base == 0) {
+		if (FUSED && tid == 0) {
 			const __amdgpu_buffer_rsrc_t rr = make_rsrc(X + (long) r * n_cols, row_bytes);
 			__builtin_amdgcn_raw_ptr_buffer_load_lds(rr, (lds_ptr_t) xlabcell, 4, 0u, (j * (uint32_t) sizeof(T)) & ~3u, 0, 0);
 		}
@@ -276,7 +284,7 @@ __device__ __forceinline__ void smx_regs(int n_rows, int n_cols, const T * X, TO
 		const __amdgpu_buffer_rsrc_t rout = make_rsrc(out + (long) row * n_cols, row_bytes);
 		/* this row: its label and the LDS part (landed: checked before the last
 		 * output pass) and the register part loaded during the last row */
-		const uint32_t lab = FUSED ? labcell[0] : 0xffffffffu;
+		const uint32_t lab = FUSED ? labcell[wave] : 0xffffffffu;
 #pragma unroll
 		for (int c = 0; c < SMX_PF; c++)
 			if (c < nch) xr[c] = pf[c * nt + tid];

@@ -137,7 +137,8 @@ def check_f32(o, v, rel=1e-5, floor=None, what=""):
     o = np.asarray(o, dtype=np.float64).ravel()
     v = np.asarray(v, dtype=np.float64).ravel()
     tol = rel * np.abs(v) + (0.0 if floor is None else np.asarray(floor, dtype=np.float64).ravel())
-    ok = (np.abs(o - v) <= tol) | (np.isnan(o) & np.isnan(v))
+    with np.errstate(invalid="ignore"):
+        ok = (np.abs(o - v) <= tol) | (np.isnan(o) & np.isnan(v)) | (o == v)
     if not ok.all():
         bad = np.flatnonzero(~ok)
         k = bad[0]

@@ -403,6 +403,63 @@ def test_softmax_cross_entropy_fused(hdl, dt, shape):
             check_f32(gm, mean, rel=1e-4, what="fused mean loss")
 
 
+def special_logits(dt, shape, seed):
+    """Rows that exercise every branch of a workgroup that walks several rows:
+    an all -inf row, rows holding +inf and NaN, and ordinary rows between."""
+    x = normal(seed, shape, std=2.0)
+    x[1, :] = -np.inf
+    x[shape[0] // 2, 17] = np.inf
+    x[shape[0] - 3, shape[1] - 1] = np.nan
+    x[4, ::3] = -np.inf
+    return to_storage(x, dt)
+
+
+# more rows than workgroups (each walks 2-3 rows with the next row, its label
+# and labelled logit in flight); 32000 and 24576 + 8 columns leave a partial
+# last chunk, 128256 is the Llama-3 vocabulary
+MANY_ROWS = [(700, 32000), (600, 24584), (300, 128256)]
+
+
+@pytest.mark.parametrize("dt", DTS, ids=dt_id)
+@pytest.mark.parametrize("shape", MANY_ROWS, ids=lambda s: "%dx%d" % s)
+def test_softmax_cross_entropy_many_rows(hdl, dt, shape):
+    from dataflow_lib_amd import api
+    n_rows, n_cols = shape
+    X = special_logits(dt, shape, seed=141)
+    labels = rng(142).integers(0, n_cols, size=n_rows).astype(np.uint32)
+    labels[0], labels[2], labels[3] = n_cols - 1, n_cols, 0xffffffff   # last column, out of range twice
+    labels[n_rows - 1] = n_cols + 100
+    labels[6] = 0
+    lo, hi, loss = np.empty(shape), np.empty(shape), np.empty(n_rows)
+    mean = np.zeros(1)
+    assert oracle().oracle_softmax_cross_entropy(dt, n_rows, n_cols, ptr(X), ptr(labels), ptr(lo), ptr(hi),
+                                                 ptr(loss), ptr(mean)) == 0
+    with Dev(hdl) as d:
+        px, pl = d.put(X), d.put(labels)
+        ploss, pmean = d.empty(4 * n_rows), d.empty(4)
+        assert api.submit_softmax_cross_entropy_loss(hdl, 0, dt, n_rows, n_cols, px, pl, ploss, pmean) == 0
+        out = d.get(px, shape, NP_STORAGE[dt])
+        gl = d.get(ploss, (n_rows,), np.float32)
+    check_rounded(out, dt, lo, hi, what="fused dlogits, many rows")
+    check_f32(gl, loss, rel=1e-4, what="fused loss, many rows")
+    assert np.isnan(gl[[1, 2, 3, n_rows - 1]]).all()
+
+
+@pytest.mark.parametrize("dt", DTS, ids=dt_id)
+@pytest.mark.parametrize("shape", MANY_ROWS[:2], ids=lambda s: "%dx%d" % s)
+def test_softmax_many_rows(hdl, dt, shape):
+    from dataflow_lib_amd import api
+    n_rows, n_cols = shape
+    X = special_logits(dt, shape, seed=151)
+    pre = np.empty(shape)
+    assert oracle().oracle_softmax(dt, dt, n_rows, n_cols, ptr(X), ptr(pre)) == 0
+    with Dev(hdl) as d:
+        px, po = d.put(X), d.empty(X.nbytes)
+        assert api.submit_softmax(hdl, 0, dt, dt, n_rows, n_cols, px, po) == 0
+        out = d.get(po, shape, NP_STORAGE[dt])
+    check_rounded(out, dt, pre, what="softmax, many rows")
+
+
 def test_softmax_cross_entropy_label_out_of_range(hdl):
     from dataflow_lib_amd import api
     dt, n_rows, n_cols = BF16, 3, 512
