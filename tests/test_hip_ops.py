@@ -70,7 +70,9 @@ def dt_id(dt):
 
 # ---------------- RMSNorm ----------------
 
-RMS_SHAPES = [(16, 4096), (64, 4096), (7, 8192), (33, 1000), (5, 8), (3, 20000)]
+# (8192, 4096) is the Llama-3-8B token batch: every workgroup walks several
+# rows there, with the next row's loads in flight across each row's reduction
+RMS_SHAPES = [(16, 4096), (64, 4096), (7, 8192), (33, 1000), (5, 8), (3, 20000), (8192, 4096)]
 
 
 def rms_inputs(dt, n_rows, n_cols, seed=1):
@@ -207,6 +209,7 @@ def test_rms_norm_bwd_repeat_is_deterministic(hdl):
 # ---------------- RoPE ----------------
 
 ROPE_CASES = [  # (tokens, q_heads, kv_heads, head_dim, theta)
+    (8192, 32, 8, 128, 500000),   # Llama-3-8B: every workgroup walks several tokens (next token prefetched)
     (64, 32, 8, 128, 500000),
     (17, 4, 2, 64, 10000),
     (9, 3, 1, 96, 500000),
@@ -272,7 +275,8 @@ def test_rope_rejects_bad_shapes(hdl):
 
 # ---------------- SwiGLU ----------------
 
-SWIGLU_SHAPES = [(33, 1000), (8, 14336), (1, 7), (3, 5)]
+# (1024, 14336): every thread runs several grid-stride steps (next step's loads in flight)
+SWIGLU_SHAPES = [(33, 1000), (8, 14336), (1, 7), (3, 5), (1024, 14336)]
 
 
 def swiglu_inputs(dt, shape, seed=71, extremes=False):
@@ -493,7 +497,9 @@ def rand_bits(seed, shape, np_t):
 
 
 @pytest.mark.parametrize("dt_np", MOVE_DTS, ids=MOVE_IDS)
-@pytest.mark.parametrize("shape", [(300, 64, 4096), (17, 1000, 1001), (5, 3, 8), (0, 10, 16)], ids=lambda s: "%dx%dx%d" % s)
+# (20000, 1000, 512): more rows than waves in the grid, so each wave gathers several
+@pytest.mark.parametrize("shape", [(300, 64, 4096), (17, 1000, 1001), (5, 3, 8), (0, 10, 16), (20000, 1000, 512)],
+                         ids=lambda s: "%dx%dx%d" % s)
 def test_embedding(hdl, dt_np, shape):
     """out[t] = table[ids[t]], bit for bit (vector path when rows are 16-byte
     multiples, element path otherwise), against the oracle's gather."""
@@ -541,6 +547,34 @@ def test_copy_to_seq_context(hdl, dt_np, kv_dim):
         pk, pv, pp, ps = d.put(K), d.put(V), d.put(pos), d.put(sizes)
         assert api.submit_copy_to_seq_context(hdl, 0, dt, n_tok * kv_dim, n_tok, kv_dim, pk, pv, pp, pptr, ps) == 0
         got = [d.get(p, (2 * S, kv_dim), np_t) for p, (S, _) in zip(dev_ctx, seqs)]
+    for g, e in zip(got, host_ctx):
+        assert np.array_equal(g, e)
+
+
+@pytest.mark.parametrize("dt_np", MOVE_DTS[1:3], ids=MOVE_IDS[1:3])
+def test_copy_to_seq_context_many_tokens(hdl, dt_np):
+    """12000 tokens of 6 packed sequences (more rows than waves in the grid,
+    so each wave scatters several), positions a shuffled 0..S-1 per sequence."""
+    from dataflow_lib_amd import api
+    dt, np_t = dt_np
+    kv_dim, S, n_seq, per_seq = 1024, 2048, 6, 2000
+    r = rng(420)
+    pos = np.concatenate([r.permutation(S)[:per_seq] for _ in range(n_seq)]).astype(np.int32)
+    which = np.repeat(np.arange(n_seq), per_seq)
+    n_tok = pos.size
+    sizes = np.full(n_tok, S, np.int32)
+    K, V = rand_bits(421, (n_tok, kv_dim), np_t), rand_bits(422, (n_tok, kv_dim), np_t)
+    sentinel = np.array(0x5A5A5A5A, np.uint32).astype(np_t)
+    host_ctx = [np.full((2 * S, kv_dim), sentinel, np_t) for _ in range(n_seq)]
+    host_ptrs = np.array([host_ctx[w].ctypes.data for w in which], np.uint64)
+    assert oracle().oracle_copy_to_seq_context(np.dtype(np_t).itemsize, n_tok * kv_dim, kv_dim, ptr(K), ptr(V), ptr(pos),
+                                               ptr(host_ptrs), ptr(sizes)) == 0
+    with Dev(hdl) as d:
+        dev_ctx = [d.put(np.full((2 * S, kv_dim), sentinel, np_t)) for _ in range(n_seq)]
+        pptr = d.put(np.array([dev_ctx[w] for w in which], np.uint64))
+        pk, pv, pp, ps = d.put(K), d.put(V), d.put(pos), d.put(sizes)
+        assert api.submit_copy_to_seq_context(hdl, 0, dt, n_tok * kv_dim, n_tok, kv_dim, pk, pv, pp, pptr, ps) == 0
+        got = [d.get(p, (2 * S, kv_dim), np_t) for p in dev_ctx]
     for g, e in zip(got, host_ctx):
         assert np.array_equal(g, e)
 
