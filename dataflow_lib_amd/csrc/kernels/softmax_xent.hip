@@ -205,23 +205,25 @@ typedef __attribute__((address_space(3))) void * lds_ptr_t;
 /* Register-resident row path, persistent over rows (row = block, block +
  * grid, ...). Chunk c of thread t is row chunk c * blockDim + t, addressed
  * through a per-row buffer resource (one VGPR offset for all chunks); the
- * whole row sits in VGPRs. The next row is requested at the top of this one
- * and lands while it computes: its first SMX_PF chunks go straight into LDS
- * (16-byte buffer loads with the LDS bit), the others into registers, and the
- * fused op's next label into an LDS cell (a 4-byte LDS load per wave; the
- * word holding the labelled logit follows the same way, for thread 0, once
- * the label is known). Each wave prefetches into and reads from its own LDS slice only, so
- * no workgroup barrier guards the buffer, and the reductions' barriers wait
- * for LDS only: the one wait for memory in a row is the one before the output
- * pass. */
+ * whole row sits in VGPRs. The next row is requested chunk by chunk during
+ * this row's max pass and lands while it computes: its first SMX_PF chunks go
+ * straight into LDS (16-byte buffer loads with the LDS bit), the others into
+ * registers, and the fused op's next label into an LDS cell (a 4-byte LDS
+ * load per wave; the word holding the labelled logit follows the same way, for
+ * thread 0, once the label is known). Each wave prefetches into and reads from
+ * its own LDS slice only, so no workgroup barrier guards the buffer, and the
+ * reductions' barriers wait for LDS only: the one wait for memory in a row is
+ * the one before the output pass. */
 template <typename T, typename TO, bool FUSED>
 __device__ __forceinline__ void smx_regs(int n_rows, int n_cols, const T * X, TO * out, const uint32_t * labels, float * loss) {
 	constexpr int VEC = VecOf<T>::N;
 	using W = SmxWord<T>;
 	using WO = SmxWord<TO>;
 	static_assert(sizeof(T) == sizeof(TO), "in-register output packing needs equal widths");
-	/* fp32 differences are not rounded, so sum exp(d) is already sum exp(x - m) */
-	constexpr bool CORR = FUSED && sizeof(T) < 4;
+	/* the loss needs sx = sum exp(x - m) over the unrounded differences; with
+	 * 16-bit storage that is not sum exp(d), so it is accumulated separately
+	 * (fp32 differences are not rounded: sx = sd) */
+	constexpr bool SX = FUSED && sizeof(T) < 4;
 	/* separate LDS cells for the max and the sum: each is rewritten only after
 	 * every wave has passed the other reduction's barrier, so reuse needs no
 	 * barrier of its own (two barriers per row) */
@@ -298,29 +300,25 @@ __device__ __forceinline__ void smx_regs(int n_rows, int n_cols, const T * X, TO
 			for (int c = SMX_PF + RP; c < SMX_MAXCH; c++)
 				if (c < nch) xr[c] = buf_load16_nt(rin, voff, c * cstride);
 		}
-		/* the whole next row is requested now and lands while this row computes */
+		/* the next row (requested during the max pass) and its label */
 		const int next = row + gridDim.x;
 		const bool has_next = next < n_rows;
 		/* the labelled logit's word: landed by the wait before the output pass,
 		 * which is also before this row is overwritten */
 		const bool lab_ok = FUSED && lab < (uint32_t) n_cols;
 		if (lab_ok) fetch_logit_word(row, lab);
-		if (has_next) {
-			const __amdgpu_buffer_rsrc_t rn = make_rsrc(X + (long) next * n_cols, row_bytes);
-#pragma unroll
-			for (int c = 0; c < SMX_PF; c++)
-				if (c < nch) __builtin_amdgcn_raw_ptr_buffer_load_lds(rn, (lds_ptr_t) &pf[c * nt + wave_base], 16, voff, c * cstride, 0, BUF_AUX_NT);
-#pragma unroll
-			for (int c = SMX_PF; c < SMX_PF + RP; c++)
-				if (c < nch) nx[c - SMX_PF] = buf_load16_nt(rn, voff, c * cstride);
-			fetch_label(next);
-		}
+		const __amdgpu_buffer_rsrc_t rn = make_rsrc(X + (long) next * n_cols, has_next ? row_bytes : 0u);
+		auto issue_next = [&](int c) {
+			if (has_next && c < nch) {
+				if (c < SMX_PF) __builtin_amdgcn_raw_ptr_buffer_load_lds(rn, (lds_ptr_t) &pf[c * nt + wave_base], 16, voff, c * cstride, 0, BUF_AUX_NT);
+				else if (c < SMX_PF + RP) nx[c - SMX_PF] = buf_load16_nt(rn, voff, c * cstride);
+			}
+		};
+		if (has_next) fetch_label(next);
 
-		/* the label sits in chunk c_lab (workgroup-uniform) of thread t_lab,
-		 * element le */
 		/* the last chunk's lanes past the row end (zeros from the range check)
-		 * become -inf, which leaves the max, the sums and the correction
-		 * unchanged, so the passes below need no per-lane mask */
+		 * become -inf, which leaves the max and both sums unchanged, so the
+		 * passes below need no per-lane mask */
 #pragma unroll
 		for (int c = 0; c < SMX_MAXCH; c++) {
 			if (c == nch - 1 && c * nt + tid >= nv) {
@@ -329,24 +327,49 @@ __device__ __forceinline__ void smx_regs(int n_rows, int n_cols, const T * X, TO
 			}
 		}
 
+		/* the label sits in chunk c_lab (workgroup-uniform) of thread t_lab,
+		 * element le */
 		const int lab_chunk = lab_ok ? (int) (lab / VEC) : 0;
 		const int c_lab = lab_ok ? lab_chunk / nt : -1;
 		const int t_lab = lab_chunk & (nt - 1);
 		const int le = (int) (lab % VEC);
 
+		/* max pass. The next row's chunk c is requested just before this row's
+		 * chunk c is used (the scheduling barrier keeps that order), so the
+		 * waves compute while the memory pipeline accepts the requests instead
+		 * of first stalling on a burst of them. For the loss, sx is summed in
+		 * the same pass online: so = sum exp(x - mref) against the running max
+		 * (mref = 0 while that is still -inf), rescaled when the max grows. */
 		float m = -__builtin_inff();
+		float mref = 0.0f, so = 0.0f;
 #pragma unroll
-		for (int c = 0; c < SMX_MAXCH; c++)
-			if (c < nch) m = chunk_max<T>(xr[c], m);
+		for (int c = 0; c < SMX_MAXCH; c++) {
+			issue_next(c);
+			__builtin_amdgcn_sched_barrier(0);
+			if (c < nch) {
+				float f[VEC];
+				unpack16<T>(xr[c], f);
+				float cm = m;
+#pragma unroll
+				for (int e = 0; e < VEC; e++) cm = __builtin_elementwise_maximum(cm, f[e]);
+				if (SX) {
+					const float mr = (cm == -__builtin_inff()) ? 0.0f : cm;
+					so *= __builtin_amdgcn_exp2f((mref - mr) * SMX_LOG2E);
+					const float nb = -mr * SMX_LOG2E;
+#pragma unroll
+					for (int e = 0; e < VEC; e++) so += __builtin_amdgcn_exp2f(fmaf(f[e], SMX_LOG2E, nb));
+					mref = mr;
+				}
+				m = cm;
+			}
+		}
 		m = cells_max(m, mslots);
+		if (SX) so *= __builtin_amdgcn_exp2f((mref - m) * SMX_LOG2E);   /* sx against the row max */
 #pragma unroll
 		for (int c = 0; c < SMX_MAXCH; c++) reg_barrier(xr[c]);
 
-		/* sd = sum exp(d) with d = rnd(x - m); the fused op also needs
-		 * sx = sum exp(x - m) = sum exp(d) * exp(delta), delta = (x - m) - d
-		 * (exact in fp32, |delta| <= half an ulp of d), taken to first order:
-		 * the neglected e^d delta^2 / 2 terms change log(sx) by < 2e-6. */
-		float sd0 = 0.0f, sd1 = 0.0f, corr = 0.0f;
+		/* sum pass: sd = sum exp(d) with d = rnd(x - m) */
+		float sd0 = 0.0f, sd1 = 0.0f;
 #pragma unroll
 		for (int c = 0; c < SMX_MAXCH; c++) {
 			if (c < nch) {
@@ -359,15 +382,13 @@ __device__ __forceinline__ void smx_regs(int n_rows, int n_cols, const T * X, TO
 					for (int e = 0; e < W::N; e++) {
 						const float ex = exp_fast(d[e]);
 						if ((i * W::N + e) & 1) sd1 += ex; else sd0 += ex;
-						/* fmaxf drops the NaN of -inf - (-inf) (where ex is 0 anyway) */
-						if (CORR) corr = fmaf(ex, fmaxf(x_m[e] - d[e], -1.0f), corr);
 					}
 				}
 				xr[c] = o;   /* d, exact in T */
 			}
 		}
 		float sd = sd0 + sd1;
-		float sx = sd + corr;
+		float sx = SX ? so : sd;
 		cells_sum2(sd, sx, sslots);
 		/* y = exp(d) / sd as one exp2: exp2(d * log2(e) - log2(sd)) */
 		const float nlog2s = -__builtin_amdgcn_logf(sd);
