@@ -137,7 +137,7 @@ static int rms_dw_finish_config(Hip_Launch_Config * c, int n_rows, int n_cols) {
 		set_1d(c, 0, 1, 0);
 		return 0;
 	}
-	set_1d(c, (unsigned) MY_CEIL(n_cols, 64), RMS_FINISH_THREADS, 0);
+	set_1d(c, (unsigned) MY_CEIL(n_cols, RMS_FIN_COLS), RMS_FINISH_THREADS, 0);
 	return 0;
 }
 

@@ -21,8 +21,9 @@
 /* launch target: bytes of row loads outstanding per CU (each row slot keeps
  * its current and next row in flight) */
 #define RMS_INFLIGHT_BYTES (64 * 1024)
-/* dW finish kernel: 64 columns per workgroup, partial rows spread over its waves */
-#define RMS_FINISH_THREADS 1024
+/* dW finish kernel: RMS_FIN_COLS columns per workgroup, partial rows spread over its threads */
+#define RMS_FINISH_THREADS 256
+#define RMS_FIN_COLS 16   /* columns per finish workgroup */
 /* fp32 partial rows for the two-pass dW reduction (16 MiB) */
 #define RMS_DW_SCRATCH_FLOATS (4u << 20)
 

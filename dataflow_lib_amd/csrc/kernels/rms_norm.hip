@@ -374,37 +374,39 @@ __device__ __forceinline__ void rms_run(const RmsArgs & a) {
 	else rms_stream<T, TW, MODE>(a, lds);
 }
 
-/* finish: dW[j] = rnd(dW[j] + sum_g partial[g][j]). A workgroup of
- * RMS_FINISH_THREADS covers 64 consecutive columns (one per lane); wave w sums
- * partial rows g = w, w + waves, ... (four loads in flight), and the wave sums
- * are added in wave order, so the result does not depend on timing. */
+/* finish: dW[j] = rnd(dW[j] + sum_g partial[g][j]). A workgroup covers
+ * RMS_FIN_COLS consecutive columns, so the grid spans the whole chip even for
+ * a few thousand columns: thread t takes column t % RMS_FIN_COLS and the
+ * partial rows g = t / RMS_FIN_COLS + k * groups, with eight loads in flight;
+ * the groups' sums are then added in group order, so the result does not
+ * depend on timing. */
 template <typename TW>
 __device__ __forceinline__ void rms_dw_finish(int n_cols, TW * dW) {
-	__shared__ float wave_part[RMS_FINISH_THREADS / 64][64];
-	const int lane = threadIdx.x & 63;
-	const int wave = threadIdx.x >> 6;
-	const int nw = blockDim.x >> 6;
-	const int j = blockIdx.x * 64 + lane;
+	constexpr int G = RMS_FINISH_THREADS / RMS_FIN_COLS;
+	__shared__ float grp_part[G][RMS_FIN_COLS];
+	const int col = threadIdx.x % RMS_FIN_COLS;
+	const int grp = threadIdx.x / RMS_FIN_COLS;
+	const int j = blockIdx.x * RMS_FIN_COLS + col;
 	const int n_parts = g_rms_dw_nparts;
 	float s = 0.0f;
 	if (j < n_cols) {
 		const float * p = g_rms_dw_partials + j;
-		int g = wave;
-		for (; g + 3 * nw < n_parts; g += 4 * nw) {
-			const float a = p[(long) g * n_cols], b = p[(long) (g + nw) * n_cols];
-			const float c = p[(long) (g + 2 * nw) * n_cols], d = p[(long) (g + 3 * nw) * n_cols];
-			s += a;
-			s += b;
-			s += c;
-			s += d;
+		int g = grp;
+		for (; g + 7 * G < n_parts; g += 8 * G) {
+			float v[8];
+#pragma unroll
+			for (int k = 0; k < 8; k++) v[k] = p[(long) (g + k * G) * n_cols];
+#pragma unroll
+			for (int k = 0; k < 8; k++) s += v[k];
 		}
-		for (; g < n_parts; g += nw) s += p[(long) g * n_cols];
+		for (; g < n_parts; g += G) s += p[(long) g * n_cols];
 	}
-	wave_part[wave][lane] = s;
+	grp_part[grp][col] = s;
 	__syncthreads();
-	if (wave == 0 && j < n_cols) {
+	if (grp == 0 && j < n_cols) {
 		float t = 0.0f;
-		for (int w = 0; w < nw; w++) t += wave_part[w][lane];
+#pragma unroll
+		for (int q = 0; q < G; q++) t += grp_part[q][col];
 		dW[j] = from_f<TW>(to_f(dW[j]) + t);
 	}
 }
