@@ -163,9 +163,6 @@ __device__ __forceinline__ void rope_slot(long n_tokens, int model_dim, int head
 	const int lane = tid & 63;
 	const bool wave0 = __builtin_amdgcn_readfirstlane(tid >> 6) == 0;
 	const int half = head_dim >> 1;
-	/* angle_p, exactly as the reference's fp32 expression
-	 * powf(theta, -((float) c / (float) head_dim)) evaluated correctly rounded */
-	for (int p = tid; p < half; p += NT) ang[p] = (float) pow((double) (float) theta, (double) -((float) (2 * p) / (float) head_dim));
 
 	const int nvq = model_dim / VEC, nvk = kv_dim / VEC;
 	const uint32_t qbytes = (uint32_t) model_dim * (uint32_t) sizeof(T), kbytes = (uint32_t) kv_dim * (uint32_t) sizeof(T);
@@ -209,12 +206,15 @@ __device__ __forceinline__ void rope_slot(long n_tokens, int model_dim, int head
 
 	long t = blockIdx.x;
 	const long stride = gridDim.x;
-	lds_barrier();   /* angles */
 	R16 q[ROPE_QJ], k[ROPE_KJ];
-	if (t < n_tokens) {
-		load(t, q, k);
-		if (wave0) table(t, 0);
-	}
+	/* the first token's chunks are requested before the angle setup, whose
+	 * fp64 pow latency then overlaps the loads */
+	if (t < n_tokens) load(t, q, k);
+	/* angle_p, exactly as the reference's fp32 expression
+	 * powf(theta, -((float) c / (float) head_dim)) evaluated correctly rounded */
+	for (int p = tid; p < half; p += NT) ang[p] = (float) pow((double) (float) theta, (double) -((float) (2 * p) / (float) head_dim));
+	lds_barrier();   /* angles */
+	if (t < n_tokens && wave0) table(t, 0);
 	lds_barrier();
 	int b = 0;
 	for (; t < n_tokens; t += stride) {
