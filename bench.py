@@ -26,6 +26,10 @@ into 4 contexts of 2048 positions). `transformer_head`: the loss-path driver
 (submit_transformer_head, training pass) at 4096 tokens x 4096 x 128256, whose
 time is its three hipBLASLt GEMMs (reported in TFLOP/s).
 
+copy_reference: per op, the code object's streaming copy moving the same
+total bytes (half read, half written), timed the same way - the ceiling the
+memory system offers that many bytes (the op's time over it is reported).
+
 cpu_baseline: the C oracle (oracle/liboracle.so, OpenMP over rows, fp64
 arithmetic) on a bounded row sample of the same ops, timed on this host.
 """
@@ -65,6 +69,25 @@ class Hip:
 
     def record(self, ev, stream):
         assert self.L.hipEventRecord(ev, stream) == 0
+
+    def module_function(self, path, name):
+        self.L.hipModuleLoad.argtypes = [ctypes.POINTER(ctypes.c_void_p), ctypes.c_char_p]
+        self.L.hipModuleGetFunction.argtypes = [ctypes.POINTER(ctypes.c_void_p), ctypes.c_void_p, ctypes.c_char_p]
+        if not hasattr(self, "modules"):
+            self.modules = {}
+        if path not in self.modules:
+            m = ctypes.c_void_p()
+            assert self.L.hipModuleLoad(ctypes.byref(m), path.encode()) == 0, path
+            self.modules[path] = m.value
+        f = ctypes.c_void_p()
+        assert self.L.hipModuleGetFunction(ctypes.byref(f), self.modules[path], name.encode()) == 0, name
+        return f.value
+
+    def launch(self, f, grid, block, args, stream):
+        self.L.hipModuleLaunchKernel.argtypes = [ctypes.c_void_p] + [ctypes.c_uint] * 7 + [
+            ctypes.c_void_p, ctypes.POINTER(ctypes.c_void_p), ctypes.c_void_p]
+        arr = (ctypes.c_void_p * len(args))(*[ctypes.cast(ctypes.pointer(a), ctypes.c_void_p) for a in args])
+        assert self.L.hipModuleLaunchKernel(f, grid, 1, 1, block, 1, 1, 0, stream, arr, None) == 0
 
     def elapsed_ms(self, a, b):
         ms = ctypes.c_float()
@@ -118,6 +141,11 @@ class Pool:
         p = self.h.alloc(nbytes)
         self.bufs.append(p)
         return p
+
+    def free(self, p):
+        self.h.sync()
+        self.bufs.remove(p)
+        self.h.free(p)
 
     def release(self):
         self.h.sync()
@@ -290,6 +318,46 @@ def time_ops(h, hip, ops, steps, warmup):
     return per_op, step_ms, wall
 
 
+def copy_reference(h, hip, pool, api, per_op, launches):
+    """What the memory system offers each op's byte count: the code object's
+    streaming copy (dataflow_stream_copy_*: non-temporal 16-byte buffer loads
+    then stores, grid-stride) moving the same total bytes half read, half
+    written, timed like the ops (back-to-back launches over rotating buffer
+    sets, >= 2 GiB per rotation, between two events); the faster of two launch
+    shapes (4 workgroups of 512 per CU with 2 chunks per step, 1 workgroup of
+    1024 per CU with 4)."""
+    stream = h.stream(0)
+    cu = h.device_info.cu_count
+    shapes = [("dataflow_stream_copy_u2_kernel", 4 * cu, 512), ("dataflow_stream_copy_u4_kernel", cu, 1024)]
+    fns = [(hip.module_function(api.KERNELS, n), g, b) for n, g, b in shapes]
+    out = {}
+    a, b = hip.event(), hip.event()
+    for name, op in per_op.items():
+        half = (op["bytes"] // 2) // 16 * 16
+        sets = max(1, min(16, (2 * GiB) // (2 * half)))
+        bufs = [(pool.empty(half), pool.empty(half)) for _ in range(sets)]
+        best = None
+        for f, grid, block in fns:
+            run = lambda i: hip.launch(f, grid, block, [ctypes.c_void_p(bufs[i % sets][0]), ctypes.c_void_p(bufs[i % sets][1]),
+                                                         ctypes.c_uint64(half // 16)], stream)
+            for i in range(3):
+                run(i)
+            hip.record(a, stream)
+            for i in range(launches):
+                run(i)
+            hip.record(b, stream)
+            h.sync()
+            us = hip.elapsed_ms(a, b) / launches * 1e3
+            best = us if best is None else min(best, us)
+        for src, dst in bufs:
+            pool.free(src)
+            pool.free(dst)
+        out[name] = {"bytes": 2 * half, "copy_us": round(best, 2),
+                     "copy_pct_of_peak": round(100.0 * 2 * half / (best * 1e-6) / 1e9 / HBM_PEAK_GBPS, 1),
+                     "op_us_over_copy_us": round(op["avg_us"] / best, 3)}
+    return out
+
+
 def time_head(h, hip, pool, api, iters):
     """submit_transformer_head, training pass (norm, output projection, fused
     loss, both backward GEMMs, norm backward) at 4096 tokens x 4096 x 128256
@@ -401,6 +469,8 @@ def main():
     ap.add_argument("--no-head", action="store_true", help="skip the transformer-head (GEMM) line")
     ap.add_argument("--cpu-budget", type=float, default=15.0, help="seconds of CPU baseline work")
     ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--no-copy-reference", action="store_true",
+                    help="skip timing the streaming copy of each op's byte count (copy_reference)")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="also run 4 device-to-device copies of 1 GiB (the HIP runtime's copy kernel), the known-size "
                          "reference for scaling rocprofv3 FETCH_SIZE / WRITE_SIZE")
@@ -422,6 +492,7 @@ def main():
         print("bench: timing %d steps after %d warmup" % (args.steps, args.warmup), file=sys.stderr, flush=True)
         per_op, step_ms, wall = time_ops(h, hip, ops, args.steps, args.warmup)
         per_extra = time_ops(h, hip, extras, max(5, args.steps // 2), 1)[0] if extras else {}
+        copy_ref = None if args.no_copy_reference else copy_reference(h, hip, pool, api, per_op, args.steps)
         head = None if args.no_head else time_head(h, hip, pool, api, 5)
         if args.copy_calibration:
             src, dst = pool.empty(GiB), pool.empty(GiB)
@@ -453,7 +524,8 @@ def main():
                                "swiglu fwd+bwd 8192x14336, fused softmax+xent 4096x128256",
                    "tokens": 8192, "hidden": 4096, "ffn": 14336, "vocab": 128256, "ce_rows": 4096},
         "pct_of_peak": round(100.0 * value / HBM_PEAK_GBPS, 1),
-        "ops": per_op, "extras": per_extra, "transformer_head": head, "roofline": roofline, "cpu_baseline": cpu,
+        "ops": per_op, "extras": per_extra, "copy_reference": copy_ref, "transformer_head": head, "roofline": roofline,
+        "cpu_baseline": cpu,
         "device": dev,
         "wall_s_timed": round(wall, 3),
     }
