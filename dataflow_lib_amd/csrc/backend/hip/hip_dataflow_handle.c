@@ -257,11 +257,23 @@ static int hip_submit_op(Dataflow_Handle * dataflow_handle, Op * op, int stream_
 		if (cfg.gridDimX == 0 || cfg.gridDimY == 0 || cfg.gridDimZ == 0) {
 			return 0;
 		}
+		Hip_Context * hc = (Hip_Context *) dataflow_handle->ctx;
+		if (f->finish_function_handle && hc->two_pass_stream != HIP_NO_STREAM && hc->two_pass_stream != stream_id) {
+			/* the previous two-pass op ran on another stream and shares the
+			 * module scratch: wait for that stream's queued work */
+			hipStream_t prev;
+			if (resolve_stream(dataflow_handle, hc->two_pass_stream, &prev, nick)) {
+				return -1;
+			}
+			HIP_CHECK_RET(hipEventRecord(hc->two_pass_event, prev), -1, "ordering op %s after the previous two-pass op", nick);
+			HIP_CHECK_RET(hipStreamWaitEvent(stream, hc->two_pass_event, 0), -1, "ordering op %s after the previous two-pass op", nick);
+		}
 		if (launch(f->function_handle, &cfg, stream, op)) {
 			fprintf(stderr, "Error: failed to launch kernel for op with nickname %s...\n", nick);
 			return -1;
 		}
 		if (f->finish_function_handle) {
+			hc->two_pass_stream = stream_id;
 			Hip_Launch_Config fcfg;
 			memset(&fcfg, 0, sizeof(fcfg));
 			if (f->set_finish_launch_config(&fcfg, dataflow_handle, f, op)) {
@@ -482,13 +494,16 @@ int init_hip_dataflow_handle(Dataflow_Handle * dataflow_handle, ComputeType comp
 
 	dataflow_handle->device_handle = malloc(sizeof(int));
 	dataflow_handle->device_info = malloc(sizeof(Hip_Device_Info));
-	dataflow_handle->ctx = malloc(sizeof(int));
+	dataflow_handle->ctx = calloc(1, sizeof(Hip_Context));
 	if (!dataflow_handle->device_handle || !dataflow_handle->device_info || !dataflow_handle->ctx) {
 		fprintf(stderr, "Error: malloc failed while creating the handle...\n");
 		return -1;
 	}
 	*((int *) dataflow_handle->device_handle) = device_id;
-	*((int *) dataflow_handle->ctx) = device_id;
+	Hip_Context * hc = (Hip_Context *) dataflow_handle->ctx;
+	hc->device_id = device_id;
+	hc->two_pass_stream = HIP_NO_STREAM;
+	HIP_CHECK_RET(hipEventCreateWithFlags(&hc->two_pass_event, hipEventDisableTiming), -1, "unable to create the two-pass ordering event on device id %d", device_id);
 	if (hip_set_device_info((Hip_Device_Info *) dataflow_handle->device_info, device_id)) {
 		fprintf(stderr, "Error: was unable to set hip device info for dev id: %d...\n", device_id);
 		return -1;
@@ -582,6 +597,8 @@ int destroy_hip_dataflow_handle(Dataflow_Handle * dataflow_handle) {
 	free(dataflow_handle->stream_states);
 	free(dataflow_handle->device_handle);
 	free(dataflow_handle->device_info);
+	Hip_Context * hc = (Hip_Context *) dataflow_handle->ctx;
+	if (hc && hc->two_pass_event) hipEventDestroy(hc->two_pass_event);
 	free(dataflow_handle->ctx);
 	dataflow_handle->streams = NULL;
 	dataflow_handle->stream_states = NULL;

@@ -14,6 +14,7 @@
 #define __HIP_PLATFORM_AMD__ 1
 #endif
 #include <hip/hip_runtime_api.h>
+#include <limits.h>
 
 #include "dataflow_common.h"
 #include "dataflow_handle.h"
@@ -87,6 +88,21 @@ struct hip_function {
 };
 
 typedef int (*Hip_Set_Func_Attribute)(Dataflow_Handle * dataflow_handle, Hip_Function * hip_function);
+
+/* What Dataflow_Handle.ctx points to (HIP has no per-handle contexts; the
+ * CUDA backend keeps its CUcontext there). The device id comes first, so ctx
+ * still reads as the device id. Two-pass ops (native ops with a finish
+ * kernel) keep per-launch partial results in their code object's
+ * module-scope scratch, so the handle orders them across its streams: a
+ * two-pass op submitted on another stream than the previous one first waits
+ * for everything then queued on that stream (an event recorded only when the
+ * stream changes, so single-stream use pays nothing). */
+#define HIP_NO_STREAM INT_MIN
+typedef struct hip_context {
+	int device_id;
+	int two_pass_stream;       /* stream id of the last two-pass op, HIP_NO_STREAM before the first */
+	hipEvent_t two_pass_event;
+} Hip_Context;
 
 /* ctx_flags is accepted for interface parity and ignored (HIP has no
  * per-handle contexts). Streams are non-blocking and all run at the default

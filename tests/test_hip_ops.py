@@ -206,6 +206,49 @@ def test_rms_norm_bwd_repeat_is_deterministic(hdl):
         assert np.array_equal(a, outs[0][0]) and np.array_equal(b.view(np.uint32), outs[0][1].view(np.uint32))
 
 
+def test_dw_ops_on_two_streams_match_one_stream(hdl):
+    """The dW ops keep their partial rows in the code object's scratch; the
+    handle orders them across streams, so a large launch on stream 0 followed
+    at once by a small one on stream 1 gives the same bits as the two run
+    one after the other."""
+    from dataflow_lib_amd import api
+    dt = BF16
+    big, small = (8192, 4096), (64, 4096)
+    ins = {}
+    for shape, seed in ((big, 61), (small, 62)):
+        X, W, ws, rs, dY, dX = rms_bwd_inputs(dt, shape[0], shape[1], seed)
+        ins[shape] = (X, W, rs, dY, dX)
+
+    def prepare(d, shape, fused):
+        X, W, rs, dY, dX = ins[shape]
+        n_cols = shape[1]
+        if fused:
+            return [d.put(a) for a in (rs, W, X, dY, dX)] + [d.put(np.zeros(n_cols, np.float32))]
+        return [d.put(a) for a in (rs, X, dY)] + [d.put(np.zeros(n_cols, np.uint16))]
+
+    def launch(p, shape, stream, fused):
+        n_rows, n_cols = shape
+        if fused:
+            assert api.submit_rms_norm_bwd(hdl, stream, dt, dt, n_rows, n_cols, 1e-5, *p) == 0
+            return p[5], (n_cols,), np.float32
+        assert api.submit_rms_norm_bwd_w(hdl, stream, dt, dt, n_rows, n_cols, 1e-5, *p) == 0
+        return p[3], (n_cols,), np.uint16
+
+    for fused_big, fused_small in ((True, False), (False, True), (False, False)):
+        outs = []
+        for stream_small in (0, 1):
+            with Dev(hdl) as d:
+                pa, pb = prepare(d, big, fused_big), prepare(d, small, fused_small)
+                hdl.sync()
+                a = launch(pa, big, 0, fused_big)
+                if stream_small == 0:
+                    hdl.sync()
+                b = launch(pb, small, stream_small, fused_small)   # stream 1: queued while the big op runs
+                outs.append((d.get(*a), d.get(*b)))
+        for r, g in zip(outs[0], outs[1]):
+            assert np.array_equal(r.view(np.uint8), g.view(np.uint8))
+
+
 # ---------------- RoPE ----------------
 
 ROPE_CASES = [  # (tokens, q_heads, kv_heads, head_dim, theta)
