@@ -322,19 +322,20 @@ def copy_reference(h, hip, pool, api, per_op, launches):
     """What the memory system offers each op's byte count: the code object's
     streaming copy (dataflow_stream_copy_*: non-temporal 16-byte buffer loads
     then stores, grid-stride) moving the same total bytes half read, half
-    written, timed like the ops (back-to-back launches over rotating buffer
-    sets, >= 2 GiB per rotation, between two events); the faster of two launch
-    shapes (4 workgroups of 512 per CU with 2 chunks per step, 1 workgroup of
-    1024 per CU with 4)."""
+    written, timed like the ops (back-to-back launches over at least two
+    rotating buffer sets, >= 2 GiB per rotation, between two events); the fastest of four
+    launch shapes (2, 3 or 4 workgroups of 512 per CU with 2 chunks per step,
+    1 workgroup of 1024 per CU with 4)."""
     stream = h.stream(0)
     cu = h.device_info.cu_count
-    shapes = [("dataflow_stream_copy_u2_kernel", 4 * cu, 512), ("dataflow_stream_copy_u4_kernel", cu, 1024)]
+    shapes = [("dataflow_stream_copy_u2_kernel", m * cu, 512) for m in (2, 3, 4)] + [
+        ("dataflow_stream_copy_u4_kernel", cu, 1024)]
     fns = [(hip.module_function(api.KERNELS, n), g, b) for n, g, b in shapes]
     out = {}
     a, b = hip.event(), hip.event()
     for name, op in per_op.items():
         half = (op["bytes"] // 2) // 16 * 16
-        sets = max(1, min(16, (2 * GiB) // (2 * half)))
+        sets = max(2, min(16, (2 * GiB) // (2 * half)))
         bufs = [(pool.empty(half), pool.empty(half)) for _ in range(sets)]
         best = None
         for f, grid, block in fns:
@@ -492,7 +493,11 @@ def main():
         print("bench: timing %d steps after %d warmup" % (args.steps, args.warmup), file=sys.stderr, flush=True)
         per_op, step_ms, wall = time_ops(h, hip, ops, args.steps, args.warmup)
         per_extra = time_ops(h, hip, extras, max(5, args.steps // 2), 1)[0] if extras else {}
-        copy_ref = None if args.no_copy_reference else copy_reference(h, hip, pool, api, per_op, args.steps)
+        copy_ref = None
+        if not args.no_copy_reference:
+            sized = dict(per_op)
+            sized.update({k: v for k, v in per_extra.items() if v["bytes"] >= (1 << 20)})
+            copy_ref = copy_reference(h, hip, pool, api, sized, args.steps)
         head = None if args.no_head else time_head(h, hip, pool, api, 5)
         if args.copy_calibration:
             src, dst = pool.empty(GiB), pool.empty(GiB)
