@@ -22,7 +22,9 @@ between two events on the launch stream. Timed as extras, outside `value`: the
 reference-compatible split ops (rms_norm_bwd_x, rms_norm_bwd_w, softmax,
 cross_entropy_loss) and the path's neighbours (embedding gather of 8192 rows
 of a 128256 x 4096 bf16 table; copy_to_seq_context of K, V [8192 x 1024] bf16
-into 4 contexts of 2048 positions). `transformer_head`: the loss-path driver
+into 4 contexts of 2048 positions; rope_copy_to_seq_context, RoPE fused with
+that scatter, on the config-3 Q, K and those contexts). `transformer_head`:
+the loss-path driver
 (submit_transformer_head, training pass) at 4096 tokens x 4096 x 128256, whose
 time is its three hipBLASLt GEMMs (reported in TFLOP/s).
 
@@ -277,6 +279,18 @@ def build_extras(h, pool, api):
         runs.append(lambda K=K, Vv=Vv, pp=pp, ptrs=ptrs, ps=ps:
                     api.submit_copy_to_seq_context(h, 0, BF16, T * 1024, T, 1024, K, Vv, pp, ptrs, ps))
     ops.append(("copy_to_seq_context", 4 * kv + T * (4 + 8 + 4), runs))
+    # --- RoPE fused with the KV-cache scatter (config 3 shapes, the contexts above):
+    # Q and K read + written, the rotated K and V written to the contexts, V read
+    q = T * 4096 * 2
+    runs = []
+    for s in range(n_sets(2 * q + 5 * kv)):
+        Q, K, Vv = pool.fill(q, "normal_bf16", 40), pool.fill(kv, "normal_bf16", 41), pool.fill(kv, "normal_bf16", 42)
+        ctx = [pool.empty(2 * 2048 * 1024 * 2) for _ in range(4)]
+        ptrs = pool.put(np.array([ctx[t // 2048] for t in range(T)], np.uint64))
+        pp, ps = pool.put(pos), pool.put(sizes)
+        runs.append(lambda Q=Q, K=K, Vv=Vv, pp=pp, ptrs=ptrs, ps=ps:
+                    api.submit_rope_copy_to_seq_context(h, 0, BF16, T * 4096, 4096, 128, 8, 500000, pp, Q, K, Vv, ptrs, ps))
+    ops.append(("rope_copy_to_seq_context", 2 * q + 5 * kv + T * (4 + 8 + 4), runs))
     return ops
 
 

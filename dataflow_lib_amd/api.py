@@ -156,6 +156,7 @@ def _declare(L):
     L.submit_rms_norm_bwd_w.argtypes = [h, s, i, i, i, i, f32, vp, vp, vp, vp]
     L.submit_rms_norm_bwd.argtypes = [h, s, i, i, i, i, f32, vp, vp, vp, vp, vp, vp]
     L.submit_rope.argtypes = [h, s, i, u64, i, i, i, i, vp, vp, vp]
+    L.submit_rope_copy_to_seq_context.argtypes = [h, s, i, u64, i, i, i, i, vp, vp, vp, vp, vp, vp]
     L.submit_rope_bwd_x.argtypes = [h, s, i, u64, i, i, i, i, vp, vp, vp]
     L.submit_swiglu.argtypes = [h, s, i, i, i, vp, vp, vp]
     L.submit_swiglu_bwd_x.argtypes = [h, s, i, i, i, i, vp, vp, vp, vp, vp]
@@ -338,6 +339,14 @@ def submit_copy_to_seq_context(handle, stream_id, fwd_dt, N, total_tokens, kv_di
                                seq_context_ptrs, seq_context_sizes):
     return lib().submit_copy_to_seq_context(_h(handle), stream_id, fwd_dt, N, total_tokens, kv_dim, X_k, X_v,
                                             seq_positions, seq_context_ptrs, seq_context_sizes)
+
+
+def submit_rope_copy_to_seq_context(handle, stream_id, fwd_dt, N, model_dim, head_dim, num_kv_heads, theta, seq_positions,
+                                    X_q, X_k, X_v, seq_context_ptrs, seq_context_sizes):
+    """RoPE forward on X_q, X_k in place and the KV-cache scatter of the rotated
+    K rows and the X_v rows, in one kernel (no reference counterpart)."""
+    return lib().submit_rope_copy_to_seq_context(_h(handle), stream_id, fwd_dt, N, model_dim, head_dim, num_kv_heads, theta,
+                                                 seq_positions, X_q, X_k, X_v, seq_context_ptrs, seq_context_sizes)
 
 
 def submit_rope(handle, stream_id, fwd_dt, N, model_dim, head_dim, num_kv_heads, theta, seq_positions, X_q, X_k):

@@ -172,7 +172,8 @@ int rms_norm_bwd_set_finish_launch_config(Hip_Launch_Config * hip_launch_config,
 
 /* ---------------- RoPE ---------------- */
 
-static int rope_config(Hip_Launch_Config * c, Dataflow_Handle * h, Hip_Function * f, Op * op, const char * what) {
+static int rope_config(Hip_Launch_Config * c, Dataflow_Handle * h, Hip_Function * f, Op * op, const char * what,
+					   unsigned long long extra_ptr_bits) {
 	const uint64_t N = ARG(op, 0, uint64_t);
 	const int model_dim = ARG(op, 1, int), head_dim = ARG(op, 2, int), num_kv_heads = ARG(op, 3, int);
 	if (model_dim <= 0 || head_dim <= 0 || (head_dim & 1) || head_dim > ROPE_MAX_HEAD_DIM || (model_dim % head_dim) != 0 ||
@@ -186,9 +187,11 @@ static int rope_config(Hip_Launch_Config * c, Dataflow_Handle * h, Hip_Function 
 	const size_t elem = arg_elem_bytes(f, 6);
 	const unsigned long long ptr_or = ptr_bits(ARG(op, 6, void *)) | ptr_bits(ARG(op, 7, void *));
 	uint64_t grid;
-	if (elem != 0 && rope_slot_ok(model_dim, num_kv_heads * head_dim, head_dim, (int) elem, ptr_or)) {
-		/* vector path: one workgroup per token at a time, persistent */
-		grid = MY_MIN(n_tokens, (uint64_t) dev(h)->cu_count * ROPE_SLOT_WG_PER_CU);
+	if (elem != 0 && rope_slot_ok(model_dim, num_kv_heads * head_dim, head_dim, (int) elem, ptr_or | extra_ptr_bits)) {
+		/* vector path: one workgroup per token at a time, persistent, as many
+		 * per CU as the kernel's registers allow (at most ROPE_SLOT_WG_PER_CU) */
+		grid = MY_MIN((uint64_t) dev(h)->cu_count * ROPE_SLOT_WG_PER_CU, (uint64_t) resident_groups(h, f, ROPE_SLOT_THREADS, 0));
+		grid = MY_MIN(n_tokens, grid);
 		set_1d(c, (unsigned) grid, ROPE_SLOT_THREADS, 0);
 		return 0;
 	}
@@ -200,11 +203,21 @@ static int rope_config(Hip_Launch_Config * c, Dataflow_Handle * h, Hip_Function 
 }
 
 int rope_set_launch_config(Hip_Launch_Config * hip_launch_config, Dataflow_Handle * dataflow_handle, Hip_Function * hip_function, Op * op) {
-	return rope_config(hip_launch_config, dataflow_handle, hip_function, op, "rope");
+	return rope_config(hip_launch_config, dataflow_handle, hip_function, op, "rope", 0ull);
 }
 
 int rope_bwd_x_set_launch_config(Hip_Launch_Config * hip_launch_config, Dataflow_Handle * dataflow_handle, Hip_Function * hip_function, Op * op) {
-	return rope_config(hip_launch_config, dataflow_handle, hip_function, op, "rope bwd x");
+	return rope_config(hip_launch_config, dataflow_handle, hip_function, op, "rope bwd x", 0ull);
+}
+
+/* RoPE + KV-cache scatter: rope's shapes, and the same path choice with the
+ * values pointer's alignment (the context rows are checked per token) */
+int rope_copy_to_seq_context_set_launch_config(Hip_Launch_Config * hip_launch_config, Dataflow_Handle * dataflow_handle, Hip_Function * hip_function, Op * op) {
+	if (ARG(op, 3, int) > 0 && (!ARG(op, 8, void *) || !ARG(op, 9, void *) || !ARG(op, 10, void *))) {
+		fprintf(stderr, "Error: rope copy to seq context: values, context pointers and context sizes are required...\n");
+		return -1;
+	}
+	return rope_config(hip_launch_config, dataflow_handle, hip_function, op, "rope copy to seq context", ptr_bits(ARG(op, 8, void *)));
 }
 
 /* ---------------- embedding / copy_to_seq_context ---------------- */

@@ -59,6 +59,10 @@ static const Native_Op_Spec native_op_specs[] = {
 	/* fused softmax + cross-entropy, no reference counterpart:
 	 * (rows, cols, logits (in place), labels, loss fp32 [rows], mean_loss fp32 [1]) */
 	{"softmax_cross_entropy_loss", NICK_FWD, 6, {I_S, I_S, ARG_FWD, DATAFLOW_UINT32, DATAFLOW_FP32, DATAFLOW_FP32}, NULL},
+	/* RoPE fused with the KV-cache scatter, no reference counterpart: rope's
+	 * 8 args, then values and copy_to_seq_context's context pointers and sizes */
+	{"rope_copy_to_seq_context", NICK_FWD, 11, {U64_S, I_S, I_S, I_S, I_S, DATAFLOW_INT, ARG_FWD, ARG_FWD, ARG_FWD,
+												 DATAFLOW_UINT64, DATAFLOW_INT}, NULL},
 };
 
 #define NUM_NATIVE_OP_SPECS ((int) (sizeof(native_op_specs) / sizeof(native_op_specs[0])))
@@ -136,6 +140,7 @@ DEFINE_FWD_BWD_SETTER(set_native_swiglu_bwd_x_skeleton, "swiglu_bwd_x")
 DEFINE_FWD_BWD_SETTER(set_native_softmax_skeleton, "softmax")
 DEFINE_BWD_SETTER(set_native_cross_entropy_loss_skeleton, "cross_entropy_loss")
 DEFINE_FWD_SETTER(set_native_softmax_cross_entropy_loss_skeleton, "softmax_cross_entropy_loss")
+DEFINE_FWD_SETTER(set_native_rope_copy_to_seq_context_skeleton, "rope_copy_to_seq_context")
 
 /* ---- registration ---- */
 
@@ -165,6 +170,7 @@ static const Native_Variant native_variants[] = {
 	PAIR3("softmax"),
 	BWD3("cross_entropy_loss"),
 	FWD3("softmax_cross_entropy_loss"),
+	FWD3("rope_copy_to_seq_context"),
 };
 
 #define NUM_NATIVE_VARIANTS ((int) (sizeof(native_variants) / sizeof(native_variants[0])))

@@ -46,9 +46,11 @@ __device__ __forceinline__ void wave_lds_sync() {
 	__builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
 }
 
-/* rotate one row (Q or K) of `width` elements with the token's table */
+/* rotate one row (Q or K) of `width` elements with the token's table; the
+ * rotated row is also written to `mirror` when it is not null (16-byte
+ * aligned on the vector path) */
 template <typename T, bool BWD, bool VECTOR>
-__device__ __forceinline__ void rope_row(T * row, int width, int head_dim, const float2 * cs, int lane) {
+__device__ __forceinline__ void rope_row(T * row, int width, int head_dim, const float2 * cs, int lane, T * mirror = nullptr) {
 	if (VECTOR) {
 		constexpr int VEC = VecOf<T>::N;
 		const int nv = width / VEC;
@@ -64,7 +66,9 @@ __device__ __forceinline__ void rope_row(T * row, int width, int head_dim, const
 				const float2 t = cs[p0 + q];
 				rotate<BWD>(t.x, t.y, f[2 * q], f[2 * q + 1], f[2 * q], f[2 * q + 1]);
 			}
-			rv[v] = pack16<T>(f);
+			const R16 o = pack16<T>(f);
+			rv[v] = o;
+			if (mirror) reinterpret_cast<R16 *>(mirror)[v] = o;
 			col += step;
 			if (col >= head_dim) col -= head_dim;
 		}
@@ -79,15 +83,53 @@ __device__ __forceinline__ void rope_row(T * row, int width, int head_dim, const
 			rotate<BWD>(t.x, t.y, to_f(row[2 * p]), to_f(row[2 * p + 1]), e2, o2);
 			row[2 * p] = from_f<T>(e2);
 			row[2 * p + 1] = from_f<T>(o2);
+			if (mirror) {
+				mirror[2 * p] = from_f<T>(e2);
+				mirror[2 * p + 1] = from_f<T>(o2);
+			}
 			col += step;
 			if (col >= head_dim) col -= head_dim;
 		}
 	}
 }
 
-template <typename T, bool BWD>
+/* Where the fused RoPE + KV-cache op puts token t's rows: the rotated K row
+ * at row pos of the token's context and its V row at row S + pos
+ * (copy_to_seq_context's layout, attention/copy_to_seq_context.cu:3-20). */
+template <typename T>
+struct KvCache {
+	const T * values;
+	const uint64_t * ctx_ptrs;
+	const int * ctx_sizes;
+	/* t is uniform over the wave, and so is the row (taken through
+	 * readfirstlane, so buffer ranges built on it live in scalar registers) */
+	__device__ __forceinline__ T * row(long t, int kv_dim, const int * seq_positions, bool value_row) const {
+		const uint64_t c = ctx_ptrs[t];
+		const uint32_t lo = __builtin_amdgcn_readfirstlane((uint32_t) c), hi = __builtin_amdgcn_readfirstlane((uint32_t) (c >> 32));
+		T * ctx = reinterpret_cast<T *>(((uint64_t) hi << 32) | lo);
+		const int p = __builtin_amdgcn_readfirstlane(seq_positions[t] + (value_row ? ctx_sizes[t] : 0));
+		return ctx + (long) p * (long) kv_dim;
+	}
+};
+
+/* one wave copies a row of n elements (16-byte chunks when both rows and the
+ * length allow it) */
+template <typename T>
+__device__ __forceinline__ void rope_copy_row(const T * src, T * dst, int n, int lane) {
+	constexpr int VEC = VecOf<T>::N;
+	if ((n % VEC) == 0 && aligned16(src) && aligned16(dst)) {
+		const R16 * s = reinterpret_cast<const R16 *>(src);
+		R16 * d = reinterpret_cast<R16 *>(dst);
+		for (int v = lane; v < n / VEC; v += 64) d[v] = s[v];
+	}
+	else {
+		for (int j = lane; j < n; j += 64) dst[j] = src[j];
+	}
+}
+
+template <typename T, bool BWD, bool KV = false>
 __device__ __forceinline__ void rope_impl(uint64_t N, int model_dim, int head_dim, int num_kv_heads, int theta,
-											const int * seq_positions, T * X_q, T * X_k) {
+											const int * seq_positions, T * X_q, T * X_k, KvCache<T> kv = KvCache<T>{}) {
 	__shared__ float2 tables[ROPE_WAVES][ROPE_MAX_HEAD_DIM / 2];
 	const int lane = threadIdx.x & 63;
 	const int wave = threadIdx.x >> 6;
@@ -126,14 +168,12 @@ __device__ __forceinline__ void rope_impl(uint64_t N, int model_dim, int head_di
 			}
 		}
 		wave_lds_sync();
-		if (vec_ok) {
-			rope_row<T, BWD, true>(X_q + t * model_dim, model_dim, head_dim, cs, lane);
-			rope_row<T, BWD, true>(X_k + t * kv_dim, kv_dim, head_dim, cs, lane);
-		}
-		else {
-			rope_row<T, BWD, false>(X_q + t * model_dim, model_dim, head_dim, cs, lane);
-			rope_row<T, BWD, false>(X_k + t * kv_dim, kv_dim, head_dim, cs, lane);
-		}
+		T * kmirror = (KV && kv_dim > 0) ? kv.row(t, kv_dim, seq_positions, false) : nullptr;
+		if (vec_ok) rope_row<T, BWD, true>(X_q + t * model_dim, model_dim, head_dim, cs, lane);
+		else rope_row<T, BWD, false>(X_q + t * model_dim, model_dim, head_dim, cs, lane);
+		if (vec_ok && (!KV || aligned16(kmirror))) rope_row<T, BWD, true>(X_k + t * kv_dim, kv_dim, head_dim, cs, lane, kmirror);
+		else rope_row<T, BWD, false>(X_k + t * kv_dim, kv_dim, head_dim, cs, lane, kmirror);
+		if (KV && kv_dim > 0) rope_copy_row<T>(kv.values + t * kv_dim, kv.row(t, kv_dim, seq_positions, true), kv_dim, lane);
 		wave_lds_sync();
 	}
 }
@@ -152,9 +192,9 @@ __device__ __forceinline__ int rope_pair_of(int chunk, int head_dim, bool pow2) 
  * half of a double-buffered LDS table, while this token is rotated and
  * stored; one barrier per token. Rows are addressed through per-row buffer
  * ranges (chunks past a row read zero and store nowhere). */
-template <typename T, bool BWD>
+template <typename T, bool BWD, bool KV = false>
 __device__ __forceinline__ void rope_slot(long n_tokens, int model_dim, int head_dim, int kv_dim, int theta,
-											const int * seq_positions, T * X_q, T * X_k) {
+											const int * seq_positions, T * X_q, T * X_k, KvCache<T> kv = KvCache<T>{}) {
 	constexpr int VEC = VecOf<T>::N;
 	constexpr int NT = ROPE_SLOT_THREADS;
 	__shared__ float ang[ROPE_MAX_HEAD_DIM / 2];
@@ -224,6 +264,30 @@ __device__ __forceinline__ void rope_slot(long n_tokens, int model_dim, int head
 			load(tn, qn, kn);
 			if (wave0) table(tn, b ^ 1);
 		}
+		/* fused KV-cache scatter: this token's V chunks and context rows (the
+		 * loads complete with the wait the rotation needs anyway) */
+		R16 v[KV ? ROPE_KJ : 1];
+		T * kctx = nullptr;
+		T * vctx = nullptr;
+		if (KV) {
+			const __amdgpu_buffer_rsrc_t rv = make_rsrc(kv.values + t * kv_dim, kbytes);
+#pragma unroll
+			for (int j = 0; j < ROPE_KJ; j++)
+				if (NT * j < nvk) v[j] = buf_load16_nt(rv, (uint32_t) (tid + NT * j) * 16u, 0);
+			/* the V loads stay ahead of the context-row loads, whose wait then
+			 * covers them: sunk next to the context stores, their own wait would
+			 * also wait for the Q/K stores issued just before */
+			__builtin_amdgcn_sched_barrier(0);
+			if (kv_dim > 0) {
+				kctx = kv.row(t, kv_dim, seq_positions, false);
+				vctx = kv.row(t, kv_dim, seq_positions, true);
+			}
+			/* the row pointers waited for every load of this wave already;
+			 * saying so lets the V stores below go without a wait of their own
+			 * (which would also wait for the Q/K stores issued before them) */
+			__builtin_amdgcn_s_waitcnt(0x0F70);   /* vmcnt(0) */
+			__builtin_amdgcn_sched_barrier(0);
+		}
 		const float2 * cs = tab[b];
 		const __amdgpu_buffer_rsrc_t rq = make_rsrc(X_q + t * model_dim, qbytes);
 		const __amdgpu_buffer_rsrc_t rk = make_rsrc(X_k + t * kv_dim, kbytes);
@@ -241,6 +305,35 @@ __device__ __forceinline__ void rope_slot(long n_tokens, int model_dim, int head
 				buf_store16_nt(rk, (uint32_t) (tid + NT * j) * 16u, 0, k[j]);
 			}
 		}
+		if (KV && kv_dim > 0) {
+			/* context rows are 16-byte aligned unless the caller's contexts
+			 * are not (a workgroup-uniform test per token) */
+			if (aligned16(kctx) && aligned16(vctx)) {
+				const __amdgpu_buffer_rsrc_t rkc = make_rsrc(kctx, kbytes), rvc = make_rsrc(vctx, kbytes);
+#pragma unroll
+				for (int j = 0; j < ROPE_KJ; j++) {
+					if (NT * j < nvk) {
+						buf_store16_nt(rkc, (uint32_t) (tid + NT * j) * 16u, 0, k[j]);
+						buf_store16_nt(rvc, (uint32_t) (tid + NT * j) * 16u, 0, v[j]);
+					}
+				}
+			}
+			else {
+#pragma unroll
+				for (int j = 0; j < ROPE_KJ; j++) {
+					const int c = tid + NT * j;
+					if (NT * j < nvk && c < nvk) {
+						const T * ke = reinterpret_cast<const T *>(&k[j]);
+						const T * ve = reinterpret_cast<const T *>(&v[j]);
+#pragma unroll
+						for (int e = 0; e < VEC; e++) {
+							kctx[c * VEC + e] = ke[e];
+							vctx[c * VEC + e] = ve[e];
+						}
+					}
+				}
+			}
+		}
 		/* tab[b ^ 1] complete, and every read of tab[b] done before it is
 		 * rebuilt; the next token's loads stay in flight across it */
 		lds_barrier();
@@ -252,15 +345,16 @@ __device__ __forceinline__ void rope_slot(long n_tokens, int model_dim, int head
 	}
 }
 
-template <typename T, bool BWD>
+template <typename T, bool BWD, bool KV = false>
 __device__ __forceinline__ void rope_dispatch(uint64_t N, int model_dim, int head_dim, int num_kv_heads, int theta,
-											const int * seq_positions, T * X_q, T * X_k) {
+											const int * seq_positions, T * X_q, T * X_k, KvCache<T> kv = KvCache<T>{}) {
 	const int kv_dim = num_kv_heads * head_dim;
-	const unsigned long long ptr_or = (unsigned long long) (uintptr_t) X_q | (unsigned long long) (uintptr_t) X_k;
+	unsigned long long ptr_or = (unsigned long long) (uintptr_t) X_q | (unsigned long long) (uintptr_t) X_k;
+	if (KV) ptr_or |= (unsigned long long) (uintptr_t) kv.values;
 	if (blockDim.x == ROPE_SLOT_THREADS && rope_slot_ok(model_dim, kv_dim, head_dim, (int) sizeof(T), ptr_or))
-		rope_slot<T, BWD>((long) (N / (uint64_t) model_dim), model_dim, head_dim, kv_dim, theta, seq_positions, X_q, X_k);
+		rope_slot<T, BWD, KV>((long) (N / (uint64_t) model_dim), model_dim, head_dim, kv_dim, theta, seq_positions, X_q, X_k, kv);
 	else
-		rope_impl<T, BWD>(N, model_dim, head_dim, num_kv_heads, theta, seq_positions, X_q, X_k);
+		rope_impl<T, BWD, KV>(N, model_dim, head_dim, num_kv_heads, theta, seq_positions, X_q, X_k, kv);
 }
 
 #define ROPE_KERNELS(SUFFIX, T)                                                                                     \
@@ -273,6 +367,21 @@ __device__ __forceinline__ void rope_dispatch(uint64_t N, int model_dim, int hea
 		rope_dispatch<T, true>(N, model_dim, head_dim, num_kv_heads, theta, seq_positions, dX_q, dX_k);             \
 	}
 
+/* RoPE fused with the KV-cache scatter (no reference counterpart; the
+ * reference notes the fusion at attention/rope.cu:50-54): rope forward on Q
+ * and K in place, and the rotated K row and the V row of token t written to
+ * rows p and S + p of its context, as copy_to_seq_context does. */
+#define ROPE_KV_KERNELS(SUFFIX, T)                                                                                  \
+	extern "C" __global__ void __launch_bounds__(256) rope_copy_to_seq_context_##SUFFIX##_kernel(uint64_t N,       \
+			int model_dim, int head_dim, int num_kv_heads, int theta, int * seq_positions, T * X_q, T * X_k,         \
+			T * values, uint64_t * seq_context_ptrs, int * seq_context_sizes) {                                      \
+		rope_dispatch<T, false, true>(N, model_dim, head_dim, num_kv_heads, theta, seq_positions, X_q, X_k,         \
+									  KvCache<T>{values, seq_context_ptrs, seq_context_sizes});                      \
+	}
+
 ROPE_KERNELS(fp32, float)
 ROPE_KERNELS(fp16, f16_t)
 ROPE_KERNELS(bf16, bf16_t)
+ROPE_KV_KERNELS(fp32, float)
+ROPE_KV_KERNELS(fp16, f16_t)
+ROPE_KV_KERNELS(bf16, bf16_t)

@@ -119,6 +119,20 @@ int submit_rope(Dataflow_Handle * handle, int stream_id,
 	return submit_built_op(handle, &op, stream_id, "rope");
 }
 
+int submit_rope_copy_to_seq_context(Dataflow_Handle * handle, int stream_id,
+						DataflowDatatype fwd_dt,
+						uint64_t N, int model_dim, int head_dim, int num_kv_heads, int theta,
+						int * seq_positions, void * X_q, void * X_k,
+						void * X_v, uint64_t * seq_context_ptrs, int * seq_context_sizes) {
+	Op op;
+	set_native_rope_copy_to_seq_context_skeleton(&op.op_skeleton, fwd_dt);
+	void ** a = op.op_args;
+	a[0] = &N; a[1] = &model_dim; a[2] = &head_dim; a[3] = &num_kv_heads; a[4] = &theta;
+	a[5] = &seq_positions; a[6] = &X_q; a[7] = &X_k;
+	a[8] = &X_v; a[9] = &seq_context_ptrs; a[10] = &seq_context_sizes;
+	return submit_built_op(handle, &op, stream_id, "rope copy to seq context");
+}
+
 int submit_rope_bwd_x(Dataflow_Handle * handle, int stream_id,
 						DataflowDatatype bwd_dt,
 						uint64_t N, int model_dim, int head_dim, int num_kv_heads, int theta,

@@ -102,6 +102,18 @@ int submit_copy_to_seq_context(Dataflow_Handle * handle, int stream_id,
 						uint64_t N, int total_tokens, int kv_dim,
 						void * X_k, void * X_v, int * seq_positions, uint64_t * seq_context_ptrs, int * seq_context_sizes);
 
+/* No reference counterpart (the fusion the reference notes at
+ * attention/rope.cu:50-54): submit_rope on X_q and X_k, then
+ * submit_copy_to_seq_context of the rotated X_k rows and the X_v rows
+ * (kv_dim = num_kv_heads * head_dim, tokens = N / model_dim), in one kernel
+ * that writes each rotated K row from registers to both places. X_v and the
+ * context arrays may be NULL only when num_kv_heads is 0. */
+int submit_rope_copy_to_seq_context(Dataflow_Handle * handle, int stream_id,
+						DataflowDatatype fwd_dt,
+						uint64_t N, int model_dim, int head_dim, int num_kv_heads, int theta,
+						int * seq_positions, void * X_q, void * X_k,
+						void * X_v, uint64_t * seq_context_ptrs, int * seq_context_sizes);
+
 /* --- mlp misc (reference: src/dataflow_ops/src/mlp_misc_ops.c:3-61) --- */
 
 /* out = silu(x_w1) * x_w3 */

@@ -33,6 +33,8 @@ int copy_to_seq_context_set_launch_config(Hip_Launch_Config * hip_launch_config,
 
 int rope_set_launch_config(Hip_Launch_Config * hip_launch_config, Dataflow_Handle * dataflow_handle, Hip_Function * hip_function, Op * op);
 int rope_bwd_x_set_launch_config(Hip_Launch_Config * hip_launch_config, Dataflow_Handle * dataflow_handle, Hip_Function * hip_function, Op * op);
+/* no reference counterpart: RoPE fused with the KV-cache scatter */
+int rope_copy_to_seq_context_set_launch_config(Hip_Launch_Config * hip_launch_config, Dataflow_Handle * dataflow_handle, Hip_Function * hip_function, Op * op);
 
 int swiglu_set_launch_config(Hip_Launch_Config * hip_launch_config, Dataflow_Handle * dataflow_handle, Hip_Function * hip_function, Op * op);
 int swiglu_bwd_x_set_launch_config(Hip_Launch_Config * hip_launch_config, Dataflow_Handle * dataflow_handle, Hip_Function * hip_function, Op * op);

@@ -64,6 +64,18 @@ void set_native_rms_norm_bwd_skeleton(Op_Skeleton * skeleton, DataflowDatatype f
  * No reference counterpart (the reference never computes a loss value). */
 void set_native_softmax_cross_entropy_loss_skeleton(Op_Skeleton * skeleton, DataflowDatatype datatype);
 
+/* RoPE forward fused with the KV-cache scatter: rope on Q and K in place,
+ * then the rotated K row and the V row of each token t written to rows p and
+ * S + p of its context (p = seq_positions[t], S = seq_context_sizes[t], the
+ * context at seq_context_ptrs[t]), as copy_to_seq_context does.
+ * Nickname "rope_copy_to_seq_context_<DT>", 11 args:
+ *   (UINT64_SCALAR N, INT_SCALAR model_dim, INT_SCALAR head_dim,
+ *    INT_SCALAR num_kv_heads, INT_SCALAR theta, INT seq_positions, dt X_q,
+ *    dt X_k, dt values, UINT64 seq_context_ptrs, INT seq_context_sizes).
+ * No reference counterpart (the reference notes the fusion at
+ * attention/rope.cu:50-54 and keeps two kernels). */
+void set_native_rope_copy_to_seq_context_skeleton(Op_Skeleton * skeleton, DataflowDatatype fwd_datatype);
+
 #ifdef __cplusplus
 }
 #endif

@@ -239,6 +239,17 @@ static int copy_to_seq_context_adapter(int elem_bytes, void ** op_args) {
 										A(6, uint64_t *), A(7, int *));
 }
 
+/* rope forward, then the scatter of the rotated K rows and the V rows */
+static int rope_copy_to_seq_context_adapter(int dt, int elem_bytes, void ** op_args) {
+	int ret = rope_adapter(dt, 0, op_args);
+	const int model_dim = A(1, int), head_dim = A(2, int), nkv = A(3, int);
+	if (ret || nkv == 0) return ret;
+	const uint64_t kv_dim = (uint64_t) nkv * (uint64_t) head_dim;
+	const uint64_t n_kv = (A(0, uint64_t) / (uint64_t) model_dim) * kv_dim;
+	return oracle_copy_to_seq_context(elem_bytes, n_kv, (int) kv_dim, A(7, void *), A(8, void *), A(5, int *),
+										A(9, uint64_t *), A(10, int *));
+}
+
 #define ADAPT_MOVE(sfx, bytes)                                                                              \
 	int embedding_##sfx##_kernel(void ** a) { return embedding_adapter(bytes, a); }                        \
 	int copy_to_seq_context_##sfx##_kernel(void ** a) { return copy_to_seq_context_adapter(bytes, a); }
@@ -249,7 +260,7 @@ ADAPT_MOVE(bf16, 2)
 ADAPT_MOVE(fp8e4m3, 1)
 ADAPT_MOVE(fp8e5m2, 1)
 
-#define ADAPT_DT(sfx, pair, code)                                                                          \
+#define ADAPT_DT(sfx, pair, code, elem)                                                                          \
 	int rms_norm_##sfx##_kernel(void ** a) { return rms_norm_adapter(code, a); }                           \
 	int rms_norm_bwd_x_##pair##_kernel(void ** a) { return rms_norm_bwd_x_adapter(code, a); }              \
 	int rms_norm_bwd_w_##pair##_kernel(void ** a) { return rms_norm_bwd_w_adapter(code, a); }              \
@@ -260,8 +271,12 @@ ADAPT_MOVE(fp8e5m2, 1)
 	int swiglu_bwd_x_##pair##_kernel(void ** a) { return swiglu_bwd_adapter(code, a); }                    \
 	int softmax_##pair##_kernel(void ** a) { return softmax_adapter(code, a); }                            \
 	int cross_entropy_loss_##sfx##_kernel(void ** a) { return cross_entropy_adapter(code, a); }            \
-	int softmax_cross_entropy_loss_##sfx##_kernel(void ** a) { return softmax_xent_adapter(code, a); }
+	int softmax_cross_entropy_loss_##sfx##_kernel(void ** a) { return softmax_xent_adapter(code, a); }      \
+	int rope_copy_to_seq_context_##sfx##_kernel(void ** a) { return rope_copy_to_seq_context_adapter(code, elem, a); }
 
-ADAPT_DT(fp32, fp32_fp32, ORACLE_FP32)
-ADAPT_DT(fp16, fp16_fp16, ORACLE_FP16)
-ADAPT_DT(bf16, bf16_bf16, ORACLE_BF16)
+#define ORACLE_FP32_BYTES 4
+#define ORACLE_FP16_BYTES 2
+#define ORACLE_BF16_BYTES 2
+ADAPT_DT(fp32, fp32_fp32, ORACLE_FP32, ORACLE_FP32_BYTES)
+ADAPT_DT(fp16, fp16_fp16, ORACLE_FP16, ORACLE_FP16_BYTES)
+ADAPT_DT(bf16, bf16_bf16, ORACLE_BF16, ORACLE_BF16_BYTES)

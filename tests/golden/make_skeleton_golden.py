@@ -33,9 +33,10 @@ SPECS = {
     "swiglu_bwd_x": ("FB", [INT_S, INT_S, F, F, B, B, B]),
     "softmax": ("FB", [INT_S, INT_S, F, B]),
     "cross_entropy_loss": ("B", [INT_S, INT_S, B, UINT32]),
-    # the two fused ops of this library (no reference counterpart)
+    # the fused ops of this library (no reference counterpart)
     "rms_norm_bwd": ("FB", [INT_S, INT_S, FP32_S, FP32, F, F, B, B, FP32]),
     "softmax_cross_entropy_loss": ("F", [INT_S, INT_S, F, UINT32, FP32, FP32]),
+    "rope_copy_to_seq_context": ("F", [UINT64_S, INT_S, INT_S, INT_S, INT_S, INT, F, F, F, 8, INT]),
 }
 
 # the reference's register_native_ops variants (set_native_op_skeletons.c:5-184)
@@ -47,7 +48,8 @@ REFERENCE_VARIANTS = ([("embedding", f, 0) for f in FWD5] + [("rms_norm", f, 0) 
                       [("rope", f, 0) for f in FWD5] + [("rope_bwd_x", 0, b) for b in BWD3] +
                       [("swiglu", f, 0) for f in FWD5] + [("swiglu_bwd_x", f, b) for f, b in COMBOS7] +
                       [("softmax", f, b) for f, b in COMBOS7] + [("cross_entropy_loss", 0, b) for b in BWD3])
-FUSED_VARIANTS = [("rms_norm_bwd", d, d) for d in BWD3] + [("softmax_cross_entropy_loss", d, 0) for d in BWD3]
+FUSED_VARIANTS = ([("rms_norm_bwd", d, d) for d in BWD3] + [("softmax_cross_entropy_loss", d, 0) for d in BWD3] +
+                  [("rope_copy_to_seq_context", d, 0) for d in BWD3])
 
 
 def header(op, fwd, bwd):

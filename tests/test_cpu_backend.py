@@ -28,8 +28,8 @@ def cpu_handle():
 
 def test_registers_every_variant(cpu_handle):
     h, n = cpu_handle
-    # 11 arithmetic ops x fp32/fp16/bf16, plus embedding and copy_to_seq_context x 5 storage types
-    assert n == 43 and h.num_ops == 43 and h.op_table.cnt == 43
+    # 12 arithmetic ops x fp32/fp16/bf16, plus embedding and copy_to_seq_context x 5 storage types
+    assert n == 46 and h.num_ops == 46 and h.op_table.cnt == 46
 
 
 def test_config1_rms_norm_fp32_through_handle(cpu_handle):
@@ -123,6 +123,25 @@ def test_embedding_and_kv_scatter_through_handle(cpu_handle):
     sizes = np.full(n_tok, S, np.int32)
     assert api.submit_copy_to_seq_context(ctypes.byref(h), 0, BF16, n_tok * kv_dim, n_tok, kv_dim, ptr(K), ptr(V), ptr(pos),
                                           ptr(ptrs), ptr(sizes)) == 0
+    assert np.array_equal(ctx[pos], K) and np.array_equal(ctx[S + pos], V)
+
+
+def test_rope_copy_to_seq_context_through_handle(cpu_handle):
+    """submit_rope_copy_to_seq_context marshals its 11 arguments the way the
+    kernel reads them: the same Q and K as submit_rope, and the context rows
+    hold the rotated K rows and the V rows."""
+    h, _ = cpu_handle
+    T, nq, nkv, hd, S = 5, 2, 1, 8, 7
+    Q, K, V = normal(310, (T, nq * hd)), normal(311, (T, nkv * hd)), normal(312, (T, nkv * hd))
+    pos = np.array([0, 4, 2, 6, 1], np.int32)
+    q2, k2 = Q.copy(), K.copy()
+    assert api.submit_rope(ctypes.byref(h), 0, FP32, T * nq * hd, nq * hd, hd, nkv, 10000, ptr(pos), ptr(q2), ptr(k2)) == 0
+    ctx = np.zeros((2 * S, nkv * hd), np.float32)
+    ptrs = np.full(T, ctx.ctypes.data, np.uint64)
+    sizes = np.full(T, S, np.int32)
+    assert api.submit_rope_copy_to_seq_context(ctypes.byref(h), 0, FP32, T * nq * hd, nq * hd, hd, nkv, 10000, ptr(pos), ptr(Q),
+                                               ptr(K), ptr(V), ptr(ptrs), ptr(sizes)) == 0
+    assert np.array_equal(Q, q2) and np.array_equal(K, k2)
     assert np.array_equal(ctx[pos], K) and np.array_equal(ctx[S + pos], V)
 
 

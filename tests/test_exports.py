@@ -51,8 +51,8 @@ def test_every_declared_symbol_is_exported():
 def test_parser_sees_the_op_api():
     names = declared_functions(os.path.join(INCLUDE, "dataflow_ops.h"))
     assert {"submit_rms_norm", "submit_rope_bwd_x", "submit_softmax_cross_entropy_loss", "submit_embedding",
-            "submit_copy_to_seq_context", "submit_matmul"} <= set(names)
-    assert len(names) == 14
+            "submit_copy_to_seq_context", "submit_matmul", "submit_rope_copy_to_seq_context"} <= set(names)
+    assert len(names) == 15
 
 
 def test_kernel_code_object_present():
@@ -60,5 +60,5 @@ def test_kernel_code_object_present():
     assert data[:4] == b"\x7fELF" or data.startswith(b"__CLANG_OFFLOAD_BUNDLE__")
     for sym in (b"rms_norm_bf16_kernel", b"rms_norm_bwd_bf16_bf16_kernel_finish", b"rope_bwd_x_bf16_kernel",
                 b"swiglu_bwd_x_bf16_bf16_kernel", b"softmax_cross_entropy_loss_bf16_kernel", b"embedding_fp8e5m2_kernel",
-                b"copy_to_seq_context_bf16_kernel"):
+                b"copy_to_seq_context_bf16_kernel", b"rope_copy_to_seq_context_bf16_kernel"):
         assert sym in data

@@ -316,6 +316,74 @@ def test_rope_rejects_bad_shapes(hdl):
         assert api.submit_rope(hdl, 0, BF16, 2048, 1024, 1024, 1, 10000, p, p, p) == -1  # head_dim > 512
 
 
+# RoPE fused with the KV-cache scatter: (tokens, q_heads, kv_heads, head_dim,
+# tokens per sequence, context byte offset). 4096 tokens walk several tokens
+# per workgroup; a context offset of one element takes the per-element stores.
+ROPE_KV_CASES = [
+    (4096, 32, 8, 128, 2048, 0),
+    (17, 4, 2, 64, 6, 0),
+    (9, 3, 1, 96, 4, 1),
+    (40, 32, 8, 128, 16, 1),
+    (5, 2, 0, 128, 3, 0),
+]
+
+
+@pytest.mark.parametrize("dt", DTS, ids=dt_id)
+@pytest.mark.parametrize("case", ROPE_KV_CASES, ids=lambda c: "T%d_q%d_kv%d_hd%d_S%d_off%d" % c)
+def test_rope_copy_to_seq_context(hdl, dt, case):
+    """Q and K rotated in place within tolerance of the oracle and bitwise
+    equal to rope followed by copy_to_seq_context on the GPU; each context
+    holds the rotated K row at row p and the V row at row S + p, every other
+    row its sentinel."""
+    from dataflow_lib_amd import api
+    T, nq, nkv, hd, per_seq, off = case
+    theta, np_t = 500000, NP_STORAGE[dt]
+    Q, K, pos = rope_inputs(dt, T, nq, nkv, hd, seed=71)
+    kv_dim = nkv * hd
+    V = to_storage(normal(74, (T, kv_dim)), dt)
+    n_seq = -(-T // per_seq)
+    S = per_seq + 3
+    seq_of = np.arange(T) // per_seq
+    pos = np.concatenate([rng(75 + s).permutation(S)[:min(per_seq, T - s * per_seq)] for s in range(n_seq)]).astype(np.int32)
+    sizes = np.full(T, S, np.int32)
+    N = T * nq * hd
+    qv, kv = np.empty(Q.shape), np.empty(K.shape)
+    assert oracle().oracle_rope(dt, 0, N, nq * hd, hd, nkv, theta, ptr(pos), ptr(Q), ptr(K), ptr(qv), ptr(kv)) == 0
+    esize = np.dtype(np_t).itemsize
+    blank = np.full((2 * S, max(kv_dim, 1) * esize), 0x5A, np.uint8).view(np_t)   # sentinel bytes
+    outs = []
+    for fused in (True, False):
+        with Dev(hdl) as d:
+            pq, pk, pv, pp, ps = d.put(Q), d.put(K), d.put(V), d.put(pos), d.put(sizes)
+            ctx = [d.put(blank, offset_bytes=off * esize) for _ in range(n_seq)]
+            pptr = d.put(np.array([ctx[s] for s in seq_of], np.uint64))
+            if fused:
+                assert api.submit_rope_copy_to_seq_context(hdl, 0, dt, N, nq * hd, hd, nkv, theta, pp, pq, pk, pv, pptr, ps) == 0
+            else:
+                assert api.submit_rope(hdl, 0, dt, N, nq * hd, hd, nkv, theta, pp, pq, pk) == 0
+                if kv_dim:
+                    assert api.submit_copy_to_seq_context(hdl, 0, dt, T * kv_dim, T, kv_dim, pk, pv, pp, pptr, ps) == 0
+            outs.append((d.get(pq, Q.shape, np_t), d.get(pk, K.shape, np_t),
+                         [d.get(c, (2 * S, max(kv_dim, 1)), np_t) for c in ctx]))
+    (gq, gk, gctx), (rq, rk, rctx) = outs
+    check_rounded(gq, dt, qv, what="fused rope Q")
+    if K.size:
+        check_rounded(gk, dt, kv, what="fused rope K")
+    assert np.array_equal(gq.view(np.uint8), rq.view(np.uint8)) and np.array_equal(gk.view(np.uint8), rk.view(np.uint8))
+    for a, b in zip(gctx, rctx):
+        assert np.array_equal(a.view(np.uint8), b.view(np.uint8))
+    if kv_dim:
+        touched = [set() for _ in range(n_seq)]
+        for t in range(T):
+            c, p = gctx[seq_of[t]], pos[t]
+            assert np.array_equal(c[p].view(np.uint8), gk[t].view(np.uint8))
+            assert np.array_equal(c[S + p].view(np.uint8), V[t].view(np.uint8))
+            touched[seq_of[t]] |= {int(p), int(S + p)}
+        for c, tset in zip(gctx, touched):
+            rest = [r for r in range(2 * S) if r not in tset]
+            assert np.array_equal(c[rest].view(np.uint8), blank[rest].view(np.uint8))
+
+
 # ---------------- SwiGLU ----------------
 
 # (1024, 14336): every thread runs several grid-stride steps (next step's loads in flight)

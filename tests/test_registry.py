@@ -113,7 +113,7 @@ def golden():
 
 def test_skeletons_match_golden_digests():
     g = golden()
-    assert len(g) == 60 and sum(s["in_reference"] for s in g) == 54
+    assert len(g) == 63 and sum(s["in_reference"] for s in g) == 54
     for s in g:
         sk = api.native_op_skeleton(s["op"], s["fwd_dt"], s["bwd_dt"])
         assert sk.header.op_nickname.decode() == s["nickname"]
