@@ -10,6 +10,7 @@
 #include "set_native_op_skeletons.h"
 
 #include <ctype.h>
+#include <stdatomic.h>
 
 /* placeholders in an argument list, resolved to the op's fwd / bwd dtype */
 #define ARG_FWD ((int) -1)
@@ -76,6 +77,18 @@ static const Native_Op_Spec * find_spec(const char * op_name) {
 	return NULL;
 }
 
+/* Fingerprints are a pure function of (op, fwd dtype, bwd dtype), so each is
+ * computed once per process and kept: every submit_* builds its op's skeleton,
+ * and the SHA-256 is most of that cost. An entry goes 0 (empty) -> 1 (being
+ * written, by the one thread that won it) -> 2 (ready); a thread that finds it
+ * not ready computes the digest itself. */
+#define FP_DT_SLOTS 32
+typedef struct {
+	_Atomic int state;
+	uint8_t fingerprint[OP_IDENTIFIER_FINGERPRINT_NUM_BYTES];
+} Fingerprint_Cache_Entry;
+static Fingerprint_Cache_Entry fingerprint_cache[NUM_NATIVE_OP_SPECS][FP_DT_SLOTS][FP_DT_SLOTS];
+
 static void build_skeleton(Op_Skeleton * skeleton, const Native_Op_Spec * spec, DataflowDatatype fwd_dt, DataflowDatatype bwd_dt) {
 	Op_Skeleton_Header * h = &skeleton->header;
 	char nick[FUNC_SYMBOL_MAX_LEN];
@@ -100,7 +113,20 @@ static void build_skeleton(Op_Skeleton * skeleton, const Native_Op_Spec * spec, 
 		int a = spec->args[i];
 		h->arg_dtypes[i] = (a == ARG_FWD) ? fwd_dt : (a == ARG_BWD) ? bwd_dt : (DataflowDatatype) a;
 	}
+	Fingerprint_Cache_Entry * e = NULL;
+	if ((unsigned) fwd_dt < FP_DT_SLOTS && (unsigned) bwd_dt < FP_DT_SLOTS) {
+		e = &fingerprint_cache[spec - native_op_specs][fwd_dt][bwd_dt];
+		if (atomic_load_explicit(&e->state, memory_order_acquire) == 2) {
+			memcpy(skeleton->identifier.fingerprint, e->fingerprint, OP_IDENTIFIER_FINGERPRINT_NUM_BYTES);
+			return;
+		}
+	}
 	do_fingerprinting(h, sizeof(Op_Skeleton_Header), skeleton->identifier.fingerprint, OP_IDENTIFIER_FINGERPRINT_TYPE);
+	int empty = 0;
+	if (e && atomic_compare_exchange_strong_explicit(&e->state, &empty, 1, memory_order_acq_rel, memory_order_relaxed)) {
+		memcpy(e->fingerprint, skeleton->identifier.fingerprint, OP_IDENTIFIER_FINGERPRINT_NUM_BYTES);
+		atomic_store_explicit(&e->state, 2, memory_order_release);
+	}
 }
 
 int set_native_op_skeleton(Op_Skeleton * skeleton, char * op_name, DataflowDatatype fwd_dt, DataflowDatatype bwd_dt) {

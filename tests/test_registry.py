@@ -121,6 +121,18 @@ def test_skeletons_match_golden_digests():
         assert hashlib.sha256(api.header_bytes(sk)).hexdigest() == s["sha256"]
 
 
+def test_cached_fingerprints_match_fresh_digests():
+    """Fingerprints are cached per (op, fwd, bwd) after the first build; later
+    builds return the same bytes, equal to SHA-256 of the rebuilt header."""
+    for s in golden():
+        for _ in range(3):
+            sk = api.native_op_skeleton(s["op"], s["fwd_dt"], s["bwd_dt"])
+            assert bytes(sk.fingerprint).hex() == s["sha256"] == hashlib.sha256(api.header_bytes(sk)).hexdigest()
+    # a dtype outside the cache's range is still fingerprinted
+    sk = api.native_op_skeleton("rope", 40)
+    assert bytes(sk.fingerprint) == hashlib.sha256(api.header_bytes(sk)).digest()
+
+
 def test_skeletons_match_reference_build_all_dtype_pairs():
     L = ref_lib()
     ops = ["embedding", "rms_norm", "rms_norm_bwd_x", "rms_norm_bwd_w", "rope", "rope_bwd_x", "copy_to_seq_context",
