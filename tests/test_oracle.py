@@ -52,9 +52,11 @@ def test_round_matches_independent_conversions():
     g = rng(1)
     v = np.concatenate([g.standard_normal(2000) * 10.0 ** g.integers(-30, 30, 2000),
                         g.standard_normal(500) * 1e-40, g.standard_normal(500) * 60000])
-    for x in v:
-        assert O.oracle_round(x, FP32) == float(np.float32(x))
-        assert O.oracle_round(x, FP16) == float(np.float16(x))
+    # values beyond the fp16 range round to inf on both sides (numpy warns on that cast)
+    with np.errstate(over="ignore"):
+        for x in v:
+            assert O.oracle_round(x, FP32) == float(np.float32(x))
+            assert O.oracle_round(x, FP16) == float(np.float16(x))
     # bf16 of fp32-representable values: integer RNE on the fp32 bit pattern
     f = v.astype(np.float32)
     f = f[np.isfinite(f)]
