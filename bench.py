@@ -337,13 +337,16 @@ def copy_reference(h, hip, pool, api, per_op, launches):
     streaming copy (dataflow_stream_copy_*: non-temporal 16-byte buffer loads
     then stores, grid-stride) moving the same total bytes half read, half
     written, timed like the ops (back-to-back launches over at least two
-    rotating buffer sets, >= 2 GiB per rotation, between two events); the fastest of four
-    launch shapes (2, 3 or 4 workgroups of 512 per CU with 2 chunks per step,
-    1 workgroup of 1024 per CU with 4)."""
+    rotating buffer sets, >= 2 GiB per rotation, between two events); the fastest of six
+    launch shapes: grid-stride with 2, 3 or 4 workgroups of 512 per CU and 2
+    chunks per step or 1 workgroup of 1024 per CU with 4; blocked (contiguous
+    blocks per workgroup, dealt round-robin) with 1 workgroup of 1024 per CU
+    and 8 chunks per thread or 2 of 512 with 16."""
     stream = h.stream(0)
     cu = h.device_info.cu_count
     shapes = [("dataflow_stream_copy_u2_kernel", m * cu, 512) for m in (2, 3, 4)] + [
-        ("dataflow_stream_copy_u4_kernel", cu, 1024)]
+        ("dataflow_stream_copy_u4_kernel", cu, 1024), ("dataflow_stream_copy_blk8_kernel", cu, 1024),
+        ("dataflow_stream_copy_blk16_kernel", 2 * cu, 512)]
     fns = [(hip.module_function(api.KERNELS, n), g, b) for n, g, b in shapes]
     out = {}
     a, b = hip.event(), hip.event()
@@ -351,8 +354,8 @@ def copy_reference(h, hip, pool, api, per_op, launches):
         half = (op["bytes"] // 2) // 16 * 16
         sets = max(2, min(16, (2 * GiB) // (2 * half)))
         bufs = [(pool.empty(half), pool.empty(half)) for _ in range(sets)]
-        best = None
-        for f, grid, block in fns:
+        best, best_shape = None, None
+        for (f, grid, block), (kname, _, _) in zip(fns, shapes):
             run = lambda i: hip.launch(f, grid, block, [ctypes.c_void_p(bufs[i % sets][0]), ctypes.c_void_p(bufs[i % sets][1]),
                                                          ctypes.c_uint64(half // 16)], stream)
             for i in range(3):
@@ -363,13 +366,14 @@ def copy_reference(h, hip, pool, api, per_op, launches):
             hip.record(b, stream)
             h.sync()
             us = hip.elapsed_ms(a, b) / launches * 1e3
-            best = us if best is None else min(best, us)
+            if best is None or us < best:
+                best, best_shape = us, "%s grid %d block %d" % (kname.replace("dataflow_stream_copy_", "").replace("_kernel", ""), grid, block)
         for src, dst in bufs:
             pool.free(src)
             pool.free(dst)
         out[name] = {"bytes": 2 * half, "copy_us": round(best, 2),
                      "copy_pct_of_peak": round(100.0 * 2 * half / (best * 1e-6) / 1e9 / HBM_PEAK_GBPS, 1),
-                     "op_us_over_copy_us": round(op["avg_us"] / best, 3)}
+                     "op_us_over_copy_us": round(op["avg_us"] / best, 3), "copy_shape": best_shape}
     return out
 
 
