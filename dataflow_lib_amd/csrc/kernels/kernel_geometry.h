@@ -45,7 +45,9 @@
 #define ROPE_SLOT_THREADS 256
 #define ROPE_QJ 4
 #define ROPE_KJ 2
-/* vector path workgroups per CU (its register use allows four) */
+/* vector path workgroups per CU at most: the RoPE kernels' registers allow
+ * four, the fused KV-cache variant's three, and the launch takes the smaller
+ * of this and what the kernel's registers leave resident */
 #define ROPE_SLOT_WG_PER_CU 4
 
 /* embedding / copy_to_seq_context: one wave per row, 4 waves per workgroup */

@@ -93,6 +93,14 @@ __device__ __forceinline__ void rope_row(T * row, int width, int head_dim, const
 	}
 }
 
+/* a wave-uniform read of read-only memory through the scalar cache (an
+ * s_load, waited for with lgkmcnt, so it does not wait behind the wave's
+ * vector-memory traffic) */
+template <typename T>
+__device__ __forceinline__ T load_scalar(const T * p) {
+	return *(const __attribute__((address_space(4))) T *) (uintptr_t) p;
+}
+
 /* Where the fused RoPE + KV-cache op puts token t's rows: the rotated K row
  * at row pos of the token's context and its V row at row S + pos
  * (copy_to_seq_context's layout, attention/copy_to_seq_context.cu:3-20). */
@@ -104,10 +112,10 @@ struct KvCache {
 	/* t is uniform over the wave, and so is the row (taken through
 	 * readfirstlane, so buffer ranges built on it live in scalar registers) */
 	__device__ __forceinline__ T * row(long t, int kv_dim, const int * seq_positions, bool value_row) const {
-		const uint64_t c = ctx_ptrs[t];
+		const uint64_t c = load_scalar(ctx_ptrs + t);
 		const uint32_t lo = __builtin_amdgcn_readfirstlane((uint32_t) c), hi = __builtin_amdgcn_readfirstlane((uint32_t) (c >> 32));
 		T * ctx = reinterpret_cast<T *>(((uint64_t) hi << 32) | lo);
-		const int p = __builtin_amdgcn_readfirstlane(seq_positions[t] + (value_row ? ctx_sizes[t] : 0));
+		const int p = __builtin_amdgcn_readfirstlane(load_scalar(seq_positions + t) + (value_row ? load_scalar(ctx_sizes + t) : 0));
 		return ctx + (long) p * (long) kv_dim;
 	}
 };
@@ -215,7 +223,7 @@ __device__ __forceinline__ void rope_slot(long n_tokens, int model_dim, int head
 
 	/* the cos/sin table of token t into tab[b] (wave 0) */
 	auto table = [&](long t, int b) {
-		const float fpos = (float) seq_positions[t];
+		const float fpos = (float) load_scalar(seq_positions + t);
 		for (int p = lane; p < half; p += 64) {
 			const float arg = fpos * ang[p];
 			double sd, cd;
@@ -223,7 +231,8 @@ __device__ __forceinline__ void rope_slot(long n_tokens, int model_dim, int head
 			tab[b][p] = make_float2((float) cd, (float) sd);
 		}
 	};
-	auto load = [&](long t, R16 (&q)[ROPE_QJ], R16 (&k)[ROPE_KJ]) {
+	constexpr int VJ = KV ? ROPE_KJ : 1;
+	auto load = [&](long t, R16 (&q)[ROPE_QJ], R16 (&k)[ROPE_KJ], R16 (&v)[VJ]) {
 		const __amdgpu_buffer_rsrc_t rq = make_rsrc(X_q + t * model_dim, qbytes);
 		const __amdgpu_buffer_rsrc_t rk = make_rsrc(X_k + t * kv_dim, kbytes);
 #pragma unroll
@@ -232,6 +241,12 @@ __device__ __forceinline__ void rope_slot(long n_tokens, int model_dim, int head
 #pragma unroll
 		for (int j = 0; j < ROPE_KJ; j++)
 			if (NT * j < nvk) k[j] = buf_load16_nt(rk, (uint32_t) (tid + NT * j) * 16u, 0);
+		if (KV) {
+			const __amdgpu_buffer_rsrc_t rv = make_rsrc(kv.values + t * kv_dim, kbytes);
+#pragma unroll
+			for (int j = 0; j < VJ; j++)
+				if (NT * j < nvk) v[j] = buf_load16_nt(rv, (uint32_t) (tid + NT * j) * 16u, 0);
+		}
 	};
 	auto rot = [&](R16 & r, int p0, const float2 * cs) {
 		float f[VEC];
@@ -246,10 +261,10 @@ __device__ __forceinline__ void rope_slot(long n_tokens, int model_dim, int head
 
 	long t = blockIdx.x;
 	const long stride = gridDim.x;
-	R16 q[ROPE_QJ], k[ROPE_KJ];
+	R16 q[ROPE_QJ], k[ROPE_KJ], v[VJ];
 	/* the first token's chunks are requested before the angle setup, whose
 	 * fp64 pow latency then overlaps the loads */
-	if (t < n_tokens) load(t, q, k);
+	if (t < n_tokens) load(t, q, k, v);
 	/* angle_p, exactly as the reference's fp32 expression
 	 * powf(theta, -((float) c / (float) head_dim)) evaluated correctly rounded */
 	for (int p = tid; p < half; p += NT) ang[p] = (float) pow((double) (float) theta, (double) -((float) (2 * p) / (float) head_dim));
@@ -259,34 +274,22 @@ __device__ __forceinline__ void rope_slot(long n_tokens, int model_dim, int head
 	int b = 0;
 	for (; t < n_tokens; t += stride) {
 		const long tn = t + stride;
-		R16 qn[ROPE_QJ], kn[ROPE_KJ];
+		/* this token's chunks (requested one token ago) have landed before the
+		 * next token's are requested, so the rotation below waits for nothing
+		 * issued after them */
+		__builtin_amdgcn_s_waitcnt(0x0F70);   /* vmcnt(0) */
+		__builtin_amdgcn_sched_barrier(0);
+		R16 qn[ROPE_QJ], kn[ROPE_KJ], vn[VJ];
 		if (tn < n_tokens) {
-			load(tn, qn, kn);
+			load(tn, qn, kn, vn);
 			if (wave0) table(tn, b ^ 1);
 		}
-		/* fused KV-cache scatter: this token's V chunks and context rows (the
-		 * loads complete with the wait the rotation needs anyway) */
-		R16 v[KV ? ROPE_KJ : 1];
+		/* fused KV-cache scatter: this token's context rows (scalar reads) */
 		T * kctx = nullptr;
 		T * vctx = nullptr;
-		if (KV) {
-			const __amdgpu_buffer_rsrc_t rv = make_rsrc(kv.values + t * kv_dim, kbytes);
-#pragma unroll
-			for (int j = 0; j < ROPE_KJ; j++)
-				if (NT * j < nvk) v[j] = buf_load16_nt(rv, (uint32_t) (tid + NT * j) * 16u, 0);
-			/* the V loads stay ahead of the context-row loads, whose wait then
-			 * covers them: sunk next to the context stores, their own wait would
-			 * also wait for the Q/K stores issued just before */
-			__builtin_amdgcn_sched_barrier(0);
-			if (kv_dim > 0) {
-				kctx = kv.row(t, kv_dim, seq_positions, false);
-				vctx = kv.row(t, kv_dim, seq_positions, true);
-			}
-			/* the row pointers waited for every load of this wave already;
-			 * saying so lets the V stores below go without a wait of their own
-			 * (which would also wait for the Q/K stores issued before them) */
-			__builtin_amdgcn_s_waitcnt(0x0F70);   /* vmcnt(0) */
-			__builtin_amdgcn_sched_barrier(0);
+		if (KV && kv_dim > 0) {
+			kctx = kv.row(t, kv_dim, seq_positions, false);
+			vctx = kv.row(t, kv_dim, seq_positions, true);
 		}
 		const float2 * cs = tab[b];
 		const __amdgpu_buffer_rsrc_t rq = make_rsrc(X_q + t * model_dim, qbytes);
@@ -341,6 +344,10 @@ __device__ __forceinline__ void rope_slot(long n_tokens, int model_dim, int head
 		for (int j = 0; j < ROPE_QJ; j++) q[j] = qn[j];
 #pragma unroll
 		for (int j = 0; j < ROPE_KJ; j++) k[j] = kn[j];
+		if (KV) {
+#pragma unroll
+			for (int j = 0; j < VJ; j++) v[j] = vn[j];
+		}
 		b ^= 1;
 	}
 }
