@@ -118,6 +118,15 @@ __device__ __forceinline__ void reg_barrier(R16 & r) {
 	__asm__ volatile("" : "+v"(r.w[0]), "+v"(r.w[1]), "+v"(r.w[2]), "+v"(r.w[3]));
 }
 
+/* A wave-uniform read of memory the kernel does not write, through the
+ * scalar cache: an s_load (a read; nothing here stores through that cache),
+ * waited for with lgkmcnt, so it does not wait behind the wave's
+ * vector-memory traffic. The address must be the same in every lane. */
+template <typename T>
+__device__ __forceinline__ T load_scalar(const T * p) {
+	return *(const __attribute__((address_space(4))) T *) (uintptr_t) p;
+}
+
 /* 16-byte global accesses with the non-temporal hint, for data each kernel
  * touches exactly once */
 __device__ __forceinline__ R16 ld16_nt(const void * p) {

@@ -67,7 +67,7 @@ __device__ __forceinline__ void embedding_impl(int num_tokens, int embed_dim, co
 	const int wpb = blockDim.x >> 6;
 	const uint32_t row_bytes = (uint32_t) embed_dim * (uint32_t) ELEM;
 	for (long t = (long) blockIdx.x * wpb + wave; t < num_tokens; t += (long) gridDim.x * wpb) {
-		const uint64_t id = token_ids[t];
+		const uint64_t id = load_scalar(token_ids + t);
 		gs_copy_row<ELEM>(static_cast<const char *>(table) + id * row_bytes, static_cast<char *>(out) + (uint64_t) t * row_bytes, row_bytes, lane);
 	}
 }
@@ -82,9 +82,11 @@ __device__ __forceinline__ void copy_to_seq_context_impl(uint64_t N, int kv_dim,
 	const long n_tokens = (long) (N / (uint64_t) kv_dim);
 	const uint32_t row_bytes = (uint32_t) kv_dim * (uint32_t) ELEM;
 	for (long t = (long) blockIdx.x * wpb + wave; t < n_tokens; t += (long) gridDim.x * wpb) {
-		char * ctx = reinterpret_cast<char *>(seq_context_ptrs[t]);
-		const uint64_t pos = (uint64_t) (int64_t) seq_positions[t];
-		const uint64_t size = (uint64_t) (int64_t) seq_context_sizes[t];
+		/* per-token metadata, wave-uniform: scalar reads (13.8 -> 13.3 us per
+		 * 8192 tokens on MI355X against vector loads) */
+		char * ctx = reinterpret_cast<char *>(load_scalar(seq_context_ptrs + t));
+		const uint64_t pos = (uint64_t) (int64_t) load_scalar(seq_positions + t);
+		const uint64_t size = (uint64_t) (int64_t) load_scalar(seq_context_sizes + t);
 		gs_copy_row<ELEM>(static_cast<const char *>(keys) + (uint64_t) t * row_bytes, ctx + pos * row_bytes, row_bytes, lane);
 		gs_copy_row<ELEM>(static_cast<const char *>(values) + (uint64_t) t * row_bytes, ctx + (size + pos) * row_bytes, row_bytes, lane);
 	}

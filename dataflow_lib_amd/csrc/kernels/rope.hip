@@ -93,14 +93,6 @@ __device__ __forceinline__ void rope_row(T * row, int width, int head_dim, const
 	}
 }
 
-/* a wave-uniform read of read-only memory through the scalar cache (an
- * s_load, waited for with lgkmcnt, so it does not wait behind the wave's
- * vector-memory traffic) */
-template <typename T>
-__device__ __forceinline__ T load_scalar(const T * p) {
-	return *(const __attribute__((address_space(4))) T *) (uintptr_t) p;
-}
-
 /* Where the fused RoPE + KV-cache op puts token t's rows: the rotated K row
  * at row pos of the token's context and its V row at row S + pos
  * (copy_to_seq_context's layout, attention/copy_to_seq_context.cu:3-20). */
