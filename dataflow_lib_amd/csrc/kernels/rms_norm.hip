@@ -380,13 +380,22 @@ __device__ __forceinline__ void rms_run(const RmsArgs & a) {
  * partial rows g = t / RMS_FIN_COLS + k * groups, with eight loads in flight;
  * the groups' sums are then added in group order, so the result does not
  * depend on timing. */
+/* XCDs of an MI355X (gfx950) */
+#define FIN_XCDS 8
+
 template <typename TW>
 __device__ __forceinline__ void rms_dw_finish(int n_cols, TW * dW) {
 	constexpr int G = RMS_FINISH_THREADS / RMS_FIN_COLS;
 	__shared__ float grp_part[G][RMS_FIN_COLS];
 	const int col = threadIdx.x % RMS_FIN_COLS;
 	const int grp = threadIdx.x / RMS_FIN_COLS;
-	const int j = blockIdx.x * RMS_FIN_COLS + col;
+	/* workgroups are dealt to the 8 XCDs round-robin, and a workgroup reads
+	 * RMS_FIN_COLS * 4 bytes of each partial row, part of a 128-byte line:
+	 * the workgroups of one XCD take adjacent column blocks so that a line's
+	 * halves meet in that XCD's L2 instead of being fetched by two XCDs */
+	const int nb = (int) gridDim.x;
+	const int cb = (nb % FIN_XCDS == 0) ? ((int) blockIdx.x % FIN_XCDS) * (nb / FIN_XCDS) + (int) blockIdx.x / FIN_XCDS : (int) blockIdx.x;
+	const int j = cb * RMS_FIN_COLS + col;
 	const int n_parts = g_rms_dw_nparts;
 	float s = 0.0f;
 	if (j < n_cols) {
