@@ -266,9 +266,11 @@ __device__ __forceinline__ void rope_slot(long n_tokens, int model_dim, int head
 	int b = 0;
 	for (; t < n_tokens; t += stride) {
 		const long tn = t + stride;
-		/* this token's chunks (requested one token ago) have landed before the
-		 * next token's are requested, so the rotation below waits for nothing
-		 * issued after them */
+		/* this token's chunks (requested one token ago) and the previous
+		 * token's stores complete here, before the next token's chunks are
+		 * requested, so the rotation below waits for nothing issued after
+		 * them (left to itself, the compiler's wait for this token's chunks
+		 * came after the next token's requests and waited for those too) */
 		__builtin_amdgcn_s_waitcnt(0x0F70);   /* vmcnt(0) */
 		__builtin_amdgcn_sched_barrier(0);
 		R16 qn[ROPE_QJ], kn[ROPE_KJ], vn[VJ];
