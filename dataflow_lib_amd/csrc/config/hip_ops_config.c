@@ -271,7 +271,8 @@ static int swiglu_config(Hip_Launch_Config * c, Dataflow_Handle * h, Hip_Functio
 	}
 	const long n = (long) rows * (long) cols;
 	const long chunks = MY_CEIL(n, (long) (16 / elem));
-	long grid = MY_CEIL(chunks, (long) SWIGLU_THREADS * SWIGLU_UNROLL);
+	/* the smaller of the two steps, so neither direction gets fewer threads than chunks per step */
+	long grid = MY_CEIL(chunks, (long) SWIGLU_THREADS * MY_MIN(SWIGLU_FWD_UNROLL, SWIGLU_BWD_UNROLL));
 	grid = MY_MIN(grid, (long) dev(h)->cu_count * SWIGLU_WG_PER_CU);
 	set_1d(c, (unsigned) grid, SWIGLU_THREADS, 0);
 	return 0;

@@ -11,8 +11,8 @@
  * finite where the reference's form gives inf - inf = NaN (g < -88.7).
  *
  * Pure streaming: the [rows x cols] tensors are treated as flat arrays,
- * grid-stride over 16-byte chunks, SWIGLU_UNROLL chunks per thread and
- * stream per step, software-pipelined: the next step's loads are issued
+ * grid-stride over 16-byte chunks, U chunks per thread and stream per step
+ * (U = SWIGLU_FWD_UNROLL / SWIGLU_BWD_UNROLL), software-pipelined: the next step's loads are issued
  * before this step's chunks are computed and stored, so every wave keeps
  * loads in flight through its arithmetic. Loads and stores are
  * non-temporal. The launch uses one large workgroup per CU so that at any
@@ -56,21 +56,21 @@ __device__ __forceinline__ void swiglu_fwd(long n, const T * g, const T * u, T *
 	const R16 * uv = reinterpret_cast<const R16 *>(u);
 	R16 * ov = reinterpret_cast<R16 *>(out);
 
-	R16 gr[SWIGLU_UNROLL], ur[SWIGLU_UNROLL];
+	R16 gr[SWIGLU_FWD_UNROLL], ur[SWIGLU_FWD_UNROLL];
 #pragma unroll
-	for (int k = 0; k < SWIGLU_UNROLL; k++) {
+	for (int k = 0; k < SWIGLU_FWD_UNROLL; k++) {
 		const long v = tid + k * nth;
 		if (v < nvec) { gr[k] = ld16_nt(gv + v); ur[k] = ld16_nt(uv + v); }
 	}
-	for (long v0 = tid; v0 < nvec; v0 += nth * SWIGLU_UNROLL) {
-		R16 gn[SWIGLU_UNROLL], un[SWIGLU_UNROLL];
+	for (long v0 = tid; v0 < nvec; v0 += nth * SWIGLU_FWD_UNROLL) {
+		R16 gn[SWIGLU_FWD_UNROLL], un[SWIGLU_FWD_UNROLL];
 #pragma unroll
-		for (int k = 0; k < SWIGLU_UNROLL; k++) {
-			const long v = v0 + (SWIGLU_UNROLL + k) * nth;
+		for (int k = 0; k < SWIGLU_FWD_UNROLL; k++) {
+			const long v = v0 + (SWIGLU_FWD_UNROLL + k) * nth;
 			if (v < nvec) { gn[k] = ld16_nt(gv + v); un[k] = ld16_nt(uv + v); }
 		}
 #pragma unroll
-		for (int k = 0; k < SWIGLU_UNROLL; k++) {
+		for (int k = 0; k < SWIGLU_FWD_UNROLL; k++) {
 			const long v = v0 + k * nth;
 			if (v < nvec) {
 				float gf[VEC], uf[VEC], of[VEC];
@@ -82,7 +82,7 @@ __device__ __forceinline__ void swiglu_fwd(long n, const T * g, const T * u, T *
 			}
 		}
 #pragma unroll
-		for (int k = 0; k < SWIGLU_UNROLL; k++) { gr[k] = gn[k]; ur[k] = un[k]; }
+		for (int k = 0; k < SWIGLU_FWD_UNROLL; k++) { gr[k] = gn[k]; ur[k] = un[k]; }
 	}
 	for (long i = nvec * VEC + tid; i < n; i += nth) {
 		out[i] = from_f<T>(swiglu_fwd_elem(to_f(g[i]), to_f(u[i])));
@@ -116,21 +116,21 @@ __device__ __forceinline__ void swiglu_bwd(long n, const T * g, const T * u, con
 	R16 * dgv = reinterpret_cast<R16 *>(dG);
 	R16 * duv = reinterpret_cast<R16 *>(dU);
 
-	R16 gr[SWIGLU_UNROLL], ur[SWIGLU_UNROLL], dr[SWIGLU_UNROLL];
+	R16 gr[SWIGLU_BWD_UNROLL], ur[SWIGLU_BWD_UNROLL], dr[SWIGLU_BWD_UNROLL];
 #pragma unroll
-	for (int k = 0; k < SWIGLU_UNROLL; k++) {
+	for (int k = 0; k < SWIGLU_BWD_UNROLL; k++) {
 		const long v = tid + k * nth;
 		if (v < nvec) { gr[k] = ld16_nt(gv + v); ur[k] = ld16_nt(uv + v); dr[k] = ld16_nt(dv + v); }
 	}
-	for (long v0 = tid; v0 < nvec; v0 += nth * SWIGLU_UNROLL) {
-		R16 gn[SWIGLU_UNROLL], un[SWIGLU_UNROLL], dn[SWIGLU_UNROLL];
+	for (long v0 = tid; v0 < nvec; v0 += nth * SWIGLU_BWD_UNROLL) {
+		R16 gn[SWIGLU_BWD_UNROLL], un[SWIGLU_BWD_UNROLL], dn[SWIGLU_BWD_UNROLL];
 #pragma unroll
-		for (int k = 0; k < SWIGLU_UNROLL; k++) {
-			const long v = v0 + (SWIGLU_UNROLL + k) * nth;
+		for (int k = 0; k < SWIGLU_BWD_UNROLL; k++) {
+			const long v = v0 + (SWIGLU_BWD_UNROLL + k) * nth;
 			if (v < nvec) { gn[k] = ld16_nt(gv + v); un[k] = ld16_nt(uv + v); dn[k] = ld16_nt(dv + v); }
 		}
 #pragma unroll
-		for (int k = 0; k < SWIGLU_UNROLL; k++) {
+		for (int k = 0; k < SWIGLU_BWD_UNROLL; k++) {
 			const long v = v0 + k * nth;
 			if (v < nvec) {
 				float gf[VEC], uf[VEC], df[VEC], ogf[VEC], ouf[VEC];
@@ -144,7 +144,7 @@ __device__ __forceinline__ void swiglu_bwd(long n, const T * g, const T * u, con
 			}
 		}
 #pragma unroll
-		for (int k = 0; k < SWIGLU_UNROLL; k++) { gr[k] = gn[k]; ur[k] = un[k]; dr[k] = dn[k]; }
+		for (int k = 0; k < SWIGLU_BWD_UNROLL; k++) { gr[k] = gn[k]; ur[k] = un[k]; dr[k] = dn[k]; }
 	}
 	for (long i = nvec * VEC + tid; i < n; i += nth) {
 		float dg, du;
