@@ -249,6 +249,42 @@ def test_dw_ops_on_two_streams_match_one_stream(hdl):
             assert np.array_equal(r.view(np.uint8), g.view(np.uint8))
 
 
+def test_fused_cross_entropy_on_two_streams_matches_one_stream(hdl):
+    """The fused loss op is a two-kernel op (its mean loss is a second,
+    deterministic kernel over the rows' losses), which the handle orders
+    across its streams: launches alternating between two streams without
+    waits give the same bits (loss, mean and dlogits) as the same launches on
+    one stream, over several rounds."""
+    from dataflow_lib_amd import api
+    dt = BF16
+    shapes = [(512, 32000), (7, 1000), (256, 128256)]
+    ins = [(logits(dt, s, seed=140 + i), rng(150 + i).integers(0, s[1], size=s[0]).astype(np.uint32))
+           for i, s in enumerate(shapes)]
+    outs = []
+    for two_streams in (False, True):
+        with Dev(hdl) as d:
+            bufs = [(d.put(X), d.put(lab), d.empty(4 * s[0]), d.empty(4)) for (X, lab), s in zip(ins, shapes)]
+            hdl.sync()
+            for rnd in range(3):
+                for i, (s, (px, pl, ploss, pmean)) in enumerate(zip(shapes, bufs)):
+                    if rnd > 0 and i == 0:
+                        hdl.sync()
+                        for (X, _), (qx, _, _, _) in zip(ins, bufs):   # fresh logits (the op works in place)
+                            hdl.to_device(np.ascontiguousarray(X), qx)
+                    stream = (i % 2) if two_streams else 0
+                    assert api.submit_softmax_cross_entropy_loss(hdl, stream, dt, s[0], s[1], px, pl, ploss, pmean) == 0
+            hdl.sync()
+            outs.append([(d.get(px, s, np.uint16), d.get(ploss, (s[0],), np.float32), d.get(pmean, (1,), np.float32))
+                         for s, (px, pl, ploss, pmean) in zip(shapes, bufs)])
+    for a, b in zip(outs[0], outs[1]):
+        for r, g in zip(a, b):
+            assert np.array_equal(r.view(np.uint8), g.view(np.uint8))
+    for (X, lab), s, (_, gl, gm) in zip(ins, shapes, outs[1]):
+        lo, hi, loss, mean = np.empty(s), np.empty(s), np.empty(s[0]), np.zeros(1)
+        assert oracle().oracle_softmax_cross_entropy(dt, s[0], s[1], ptr(X), ptr(lab), ptr(lo), ptr(hi), ptr(loss), ptr(mean)) == 0
+        check_f32(gm, mean, rel=1e-4, what="mean loss")
+
+
 # ---------------- RoPE ----------------
 
 ROPE_CASES = [  # (tokens, q_heads, kv_heads, head_dim, theta)
