@@ -68,11 +68,21 @@ def dt_id(dt):
     return DT_IDS[dt]
 
 
+# Seeded random shapes added to each op's fixed list (the same every run; the
+# test id shows them), so each family also runs on shapes nobody picked.
+_SHAPE_RNG = np.random.default_rng(20261201)
+
+
+def _ri(lo, hi):
+    return int(_SHAPE_RNG.integers(lo, hi + 1))
+
+
 # ---------------- RMSNorm ----------------
 
 # (8192, 4096) is the Llama-3-8B token batch: every workgroup walks several
 # rows there, with the next row's loads in flight across each row's reduction
 RMS_SHAPES = [(16, 4096), (64, 4096), (7, 8192), (33, 1000), (5, 8), (3, 20000), (8192, 4096)]
+RMS_SHAPES += [(_ri(1, 2000), 8 * _ri(1, 1024)), (_ri(1, 300), _ri(1, 9000)), (_ri(500, 3000), 8 * _ri(200, 700))]
 
 
 def rms_inputs(dt, n_rows, n_cols, seed=1):
@@ -295,6 +305,9 @@ ROPE_CASES = [  # (tokens, q_heads, kv_heads, head_dim, theta)
     (5, 2, 2, 6, 10000),
     (3, 2, 0, 128, 500000),
 ]
+for _ in range(3):
+    _nq = _ri(1, 40)
+    ROPE_CASES.append((_ri(1, 3000), _nq, _ri(0, _nq), 2 * _ri(1, 128), 500000))
 
 
 def rope_inputs(dt, T, nq, nkv, hd, seed=51):
@@ -362,6 +375,9 @@ ROPE_KV_CASES = [
     (40, 32, 8, 128, 16, 1),
     (5, 2, 0, 128, 3, 0),
 ]
+for _ in range(2):
+    _nq = _ri(1, 32)
+    ROPE_KV_CASES.append((_ri(1, 2000), _nq, _ri(1, _nq), 8 * _ri(1, 32), _ri(1, 600), _ri(0, 1)))
 
 
 @pytest.mark.parametrize("dt", DTS, ids=dt_id)
@@ -424,6 +440,7 @@ def test_rope_copy_to_seq_context(hdl, dt, case):
 
 # (1024, 14336): every thread runs several grid-stride steps (next step's loads in flight)
 SWIGLU_SHAPES = [(33, 1000), (8, 14336), (1, 7), (3, 5), (1024, 14336)]
+SWIGLU_SHAPES += [(_ri(1, 600), _ri(1, 20000)), (_ri(1, 64), 8 * _ri(1, 2000))]
 
 
 def swiglu_inputs(dt, shape, seed=71, extremes=False):
@@ -486,6 +503,7 @@ def test_swiglu_unaligned(hdl):
 # ---------------- softmax / cross-entropy ----------------
 
 SMX_SHAPES = [(4, 128256), (3, 1000), (2, 1001), (2, 140000), (5, 64), (1, 1)]
+SMX_SHAPES += [(_ri(1, 40), _ri(1, 150000)), (_ri(1, 40), 8 * _ri(1, 16384))]
 
 
 def logits(dt, shape, seed=101):
@@ -569,6 +587,7 @@ def special_logits(dt, shape, seed):
 # and labelled logit in flight); 32000 and 24576 + 8 columns leave a partial
 # last chunk, 128256 is the Llama-3 vocabulary
 MANY_ROWS = [(700, 32000), (600, 24584), (300, 128256)]
+MANY_ROWS += [(_ri(257, 700), 8 * _ri(125, 16032))]
 
 
 @pytest.mark.parametrize("dt", DTS, ids=dt_id)
