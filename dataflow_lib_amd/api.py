@@ -111,7 +111,11 @@ _VT_TYPES = {
     "submit_peer_transfer": ctypes.CFUNCTYPE(ctypes.c_int, _H, ctypes.c_int, _P, _P, ctypes.c_uint64),
     "get_stream_state": ctypes.CFUNCTYPE(_P, _H, ctypes.c_int),
     "submit_dependency": ctypes.CFUNCTYPE(ctypes.c_int, _H, ctypes.c_int, _P),
+    "submit_host_op": ctypes.CFUNCTYPE(ctypes.c_int, _H, _P, _P, ctypes.c_int),
 }
+
+# host functions for submit_host_op: void fn(void * arg)
+HostFunc = ctypes.CFUNCTYPE(None, ctypes.c_void_p)
 
 # ---- library ----
 _lib = None
@@ -249,6 +253,19 @@ class Handle:
 
     def copy(self, dst, src, nbytes, stream_id=-1):
         return self._fns["submit_peer_transfer"](self.ref, stream_id, dst, src, nbytes)
+
+    def stream_state(self, stream_id):
+        """get_stream_state: an event recorded now on the stream (NULL on error)."""
+        return self._fns["get_stream_state"](self.ref, stream_id)
+
+    def submit_dependency(self, stream_id, state):
+        """submit_dependency: the stream waits for a state from stream_state."""
+        return self._fns["submit_dependency"](self.ref, stream_id, state)
+
+    def submit_host_op(self, fn, arg, stream_id=0):
+        """submit_host_op: `fn` (a HostFunc; the caller keeps it alive) runs on a
+        runtime thread once the stream's earlier work is done."""
+        return self._fns["submit_host_op"](self.ref, ctypes.cast(fn, ctypes.c_void_p), arg, stream_id)
 
     def sync_stream(self, stream_id=0):
         return self._fns["sync_stream"](self.ref, stream_id)
