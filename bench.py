@@ -496,7 +496,8 @@ def main():
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
         print("bench.py measures one GPU only: every GPU box here has a single MI355X and this build has no "
-              "multi-GPU path (the ops are token-sharded with no exchange; see DESIGN.md). Run with --gpus 1.",
+              "multi-GPU path (the ops shard by tokens with no exchange; only the dW and mean-loss sums would cross GPUs). "
+              "Run with --gpus 1.",
               file=sys.stderr)
         sys.exit(2)
     from dataflow_lib_amd import api
