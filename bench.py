@@ -294,14 +294,14 @@ def build_extras(h, pool, api):
     return ops
 
 
-def time_ops(h, hip, ops, steps, warmup):
+def time_ops(h, hip, ops, steps, warmup, batches=5):
     """Time `steps` steps (each op once per step, rotating buffer sets) on one
     stream, with events only at the two ends (an event recorded between
     kernels costs the stream several microseconds, which would be counted as
     the ops' time). Then, for the per-op figures, each op alone: `steps`
-    launches back to back over its rotating sets, again timed from two events;
-    the op's time is the average launch duration (kernel plus the gap to the
-    next launch)."""
+    launches back to back over its rotating sets, again timed from two events,
+    in `batches` batches; the op's time is the median batch's average launch
+    duration (kernel plus the gap to the next launch)."""
     stream = h.stream(0)
     for w in range(warmup):
         for name, _, runs in ops:
@@ -319,13 +319,17 @@ def time_ops(h, hip, ops, steps, warmup):
     step_ms = hip.elapsed_ms(a, b) / steps
     per_op = {}
     for name, nbytes, runs in ops:
-        hip.record(a, stream)
-        for k in range(steps):
-            assert runs[k % len(runs)]() == 0, name
-        hip.record(b, stream)
-        h.sync()
-        avg = hip.elapsed_ms(a, b) / steps
-        per_op[name] = {"bytes": nbytes, "avg_us": round(avg * 1e3, 2), "launches": steps,
+        avgs = []
+        for _ in range(batches):
+            hip.record(a, stream)
+            for k in range(steps):
+                assert runs[k % len(runs)]() == 0, name
+            hip.record(b, stream)
+            h.sync()
+            avgs.append(hip.elapsed_ms(a, b) / steps)
+        avg = sorted(avgs)[len(avgs) // 2]
+        per_op[name] = {"bytes": nbytes, "avg_us": round(avg * 1e3, 2), "launches": steps, "batches": batches,
+                        "batch_us_min_max": [round(min(avgs) * 1e3, 2), round(max(avgs) * 1e3, 2)],
                         "gbps": round(nbytes / (avg * 1e-3) / 1e9, 1),
                         "pct_of_peak": round(100.0 * nbytes / (avg * 1e-3) / 1e9 / HBM_PEAK_GBPS, 1),
                         "rotating_sets": len(runs)}
@@ -337,7 +341,8 @@ def copy_reference(h, hip, pool, api, per_op, launches):
     streaming copy (dataflow_stream_copy_*: non-temporal 16-byte buffer loads
     then stores, grid-stride) moving the same total bytes half read, half
     written, timed like the ops (back-to-back launches over at least two
-    rotating buffer sets, >= 2 GiB per rotation, between two events); the fastest of six
+    rotating buffer sets, >= 2 GiB per rotation, between two events; median of three
+    batches per shape); the fastest of six
     launch shapes: grid-stride with 2, 3 or 4 workgroups of 512 per CU and 2
     chunks per step or 1 workgroup of 1024 per CU with 4; blocked (contiguous
     blocks per workgroup, dealt round-robin) with 1 workgroup of 1024 per CU
@@ -360,12 +365,15 @@ def copy_reference(h, hip, pool, api, per_op, launches):
                                                          ctypes.c_uint64(half // 16)], stream)
             for i in range(3):
                 run(i)
-            hip.record(a, stream)
-            for i in range(launches):
-                run(i)
-            hip.record(b, stream)
-            h.sync()
-            us = hip.elapsed_ms(a, b) / launches * 1e3
+            batch = []
+            for _ in range(3):
+                hip.record(a, stream)
+                for i in range(launches):
+                    run(i)
+                hip.record(b, stream)
+                h.sync()
+                batch.append(hip.elapsed_ms(a, b) / launches * 1e3)
+            us = sorted(batch)[1]   # median of three batches, so the fastest shape is not a lucky batch
             if best is None or us < best:
                 best, best_shape = us, "%s grid %d block %d" % (kname.replace("dataflow_stream_copy_", "").replace("_kernel", ""), grid, block)
         for src, dst in bufs:
@@ -465,7 +473,19 @@ def cpu_baseline(budget_s):
         reps += 1
         if time.perf_counter() - t_start > budget_s or reps >= 1000:
             break
+    model, flags = "", []
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name") and not model:
+                    model = line.split(":", 1)[1].strip()
+                elif line.startswith("flags") and not flags:
+                    have = set(line.split(":", 1)[1].split())
+                    flags = [x for x in ("avx2", "fma", "avx512f", "avx512bw", "avx512_bf16", "avx512_fp16") if x in have]
+    except OSError:
+        pass
     return {"value": round(tot_b / tot_t / 1e9, 3), "unit": "GB/s", "cores": int(O.oracle_num_threads()), "kind": "port",
+            "nproc": os.cpu_count(), "cpu_model": model, "isa": flags,
             "sample": "oracle/liboracle.so (C, fp64, OpenMP over rows) on %d-row slices of configs 2-4 and %d rows of config 5, "
                       "%d repetitions, same byte formulas" % (rows, ce_rows, reps),
             "ops": {k: round(v[0] / v[1] / 1e9, 3) for k, v in per.items()}}

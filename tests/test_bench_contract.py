@@ -33,6 +33,7 @@ def test_cpu_baseline_object():
     assert cpu["kind"] == "port" and cpu["unit"] == "GB/s"
     assert cpu["value"] > 0 and cpu["cores"] >= 1
     assert "oracle" in cpu["sample"]
+    assert cpu["nproc"] >= 1 and isinstance(cpu["cpu_model"], str) and isinstance(cpu["isa"], list)
     assert sorted(cpu["ops"]) == sorted(STEP_OPS)
     assert all(v > 0 for v in cpu["ops"].values())
 
