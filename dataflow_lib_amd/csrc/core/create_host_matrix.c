@@ -39,7 +39,7 @@ static void * dest_or_alloc(void * opt_dest, uint64_t num_els, DataflowDatatype 
 		return NULL;
 	}
 	if (opt_dest) return opt_dest;
-	void * p = malloc((num_els * el) ? num_els * el : 1);
+	void * p = malloc((num_els * el != 0) ? num_els * el : 1);
 	if (!p) fprintf(stderr, "Error: %s: could not allocate %lu elements on the host...\n", what, (unsigned long) num_els);
 	return p;
 }
@@ -113,7 +113,7 @@ void * load_host_matrix_from_file(char * filepath, uint64_t M, uint64_t N, Dataf
 		fprintf(stderr, "Error: could not load matrix from file: %s\n", filepath);
 		return NULL;
 	}
-	void * orig = malloc((n * el) ? n * el : 1);
+	void * orig = malloc((n * el != 0) ? n * el : 1);
 	if (!orig) {
 		fprintf(stderr, "Error: load host matrix: could not allocate %lu elements...\n", (unsigned long) n);
 		fclose(fp);
