@@ -471,6 +471,13 @@ static int hip_set_device_info(Hip_Device_Info * info, int device_id) {
 	return 0;
 }
 
+/* a failed initialisation releases what it had created (destroy handles the
+ * fields that are still NULL) and reports -1 */
+static int init_fail(Dataflow_Handle * dataflow_handle) {
+	destroy_hip_dataflow_handle(dataflow_handle);
+	return -1;
+}
+
 int init_hip_dataflow_handle(Dataflow_Handle * dataflow_handle, ComputeType compute_type, int device_id,
 								int ctx_id, unsigned int ctx_flags,
 								int num_streams, int * opt_stream_prios, char ** opt_stream_names) {
@@ -497,16 +504,16 @@ int init_hip_dataflow_handle(Dataflow_Handle * dataflow_handle, ComputeType comp
 	dataflow_handle->ctx = calloc(1, sizeof(Hip_Context));
 	if (!dataflow_handle->device_handle || !dataflow_handle->device_info || !dataflow_handle->ctx) {
 		fprintf(stderr, "Error: malloc failed while creating the handle...\n");
-		return -1;
+		return init_fail(dataflow_handle);
 	}
 	*((int *) dataflow_handle->device_handle) = device_id;
 	Hip_Context * hc = (Hip_Context *) dataflow_handle->ctx;
 	hc->device_id = device_id;
 	hc->two_pass_stream = HIP_NO_STREAM;
-	HIP_CHECK_RET(hipEventCreateWithFlags(&hc->two_pass_event, hipEventDisableTiming), -1, "unable to create the two-pass ordering event on device id %d", device_id);
+	HIP_CHECK_RET(hipEventCreateWithFlags(&hc->two_pass_event, hipEventDisableTiming), init_fail(dataflow_handle), "unable to create the two-pass ordering event on device id %d", device_id);
 	if (hip_set_device_info((Hip_Device_Info *) dataflow_handle->device_info, device_id)) {
 		fprintf(stderr, "Error: was unable to set hip device info for dev id: %d...\n", device_id);
-		return -1;
+		return init_fail(dataflow_handle);
 	}
 
 	dataflow_handle->num_streams = num_streams;
@@ -522,7 +529,7 @@ int init_hip_dataflow_handle(Dataflow_Handle * dataflow_handle, ComputeType comp
 			dataflow_handle->stream_names[i] = strdup(opt_stream_names[i]);
 			if (!dataflow_handle->stream_names[i]) {
 				fprintf(stderr, "Error: failed to alloc space to hold stream name...\n");
-				return -1;
+				return init_fail(dataflow_handle);
 			}
 		}
 	}
@@ -532,13 +539,13 @@ int init_hip_dataflow_handle(Dataflow_Handle * dataflow_handle, ComputeType comp
 	dataflow_handle->stream_states = calloc(ns, sizeof(hipEvent_t));
 	if (!dataflow_handle->streams || !dataflow_handle->stream_states) {
 		fprintf(stderr, "Error: malloc failed to allocate stream containers...\n");
-		return -1;
+		return init_fail(dataflow_handle);
 	}
 	hipStream_t * streams = (hipStream_t *) dataflow_handle->streams;
 	hipEvent_t * events = (hipEvent_t *) dataflow_handle->stream_states;
 	for (int i = 0; i < num_streams; i++) {
-		HIP_CHECK_RET(hipStreamCreateWithFlags(&streams[i], hipStreamNonBlocking), -1, "unable to initialize stream #%d on device id %d", i, device_id);
-		HIP_CHECK_RET(hipEventCreateWithFlags(&events[i], hipEventDisableTiming), -1, "unable to initialize event for stream #%d on device id %d", i, device_id);
+		HIP_CHECK_RET(hipStreamCreateWithFlags(&streams[i], hipStreamNonBlocking), init_fail(dataflow_handle), "unable to initialize stream #%d on device id %d", i, device_id);
+		HIP_CHECK_RET(hipEventCreateWithFlags(&events[i], hipEventDisableTiming), init_fail(dataflow_handle), "unable to initialize event for stream #%d on device id %d", i, device_id);
 	}
 
 	dataflow_handle->num_native_function_libs = 0;
@@ -546,7 +553,7 @@ int init_hip_dataflow_handle(Dataflow_Handle * dataflow_handle, ComputeType comp
 	if (init_table(&dataflow_handle->op_table, hip_op_table_hash_func, OP_IDENTIFIER_FINGERPRINT_NUM_BYTES, sizeof(Hip_Function),
 					OP_TABLE_MIN_SIZE, OP_TABLE_MAX_SIZE, 1.0f, 1.0f)) {
 		fprintf(stderr, "Error: failed to init op table...\n");
-		return -1;
+		return init_fail(dataflow_handle);
 	}
 
 	dataflow_handle->register_native_code = hip_register_native_code;
