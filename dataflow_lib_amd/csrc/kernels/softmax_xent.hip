@@ -488,65 +488,92 @@ __device__ __forceinline__ void smx_stream(int n_rows, int n_cols, const T * X, 
 	}
 }
 
-/* fp32 rows longer than the register path holds (more than SMX_MAXCH 16-byte
- * chunks per thread), 16-byte aligned: two passes over the row instead of
- * three. x - m is not rounded in fp32, so the row's max and sum come from one
- * pass, online: each thread keeps its running max and its sum against it
- * (rescaled when the max grows; mref = 0 while the max is still -inf), and
- * the workgroup combines them against the row max. The second pass writes
- * exp(x - m) / s with the register path's expression. The first pass reads
- * with the default cache policy, so the second finds the row in cache where
- * it can. The labelled logit is taken from the first pass's registers by the
- * thread holding it (the row may be overwritten in place by the second). */
-template <bool FUSED>
-__device__ __forceinline__ void smx_stream_f32(int n_rows, int n_cols, const float * X, float * out, const uint32_t * labels, float * loss) {
+/* Rows longer than the register path holds (more than SMX_MAXCH 16-byte
+ * chunks per thread), 16-byte aligned: streaming passes over the row with
+ * 16-byte accesses. The first pass finds the row max and, online, the sum of
+ * exp(x - m) over the unrounded differences (each thread keeps its running
+ * max and its sum against it, rescaled when the max grows; mref = 0 while the
+ * max is still -inf; the workgroup combines them against the row max). In
+ * fp32, x - m is not rounded, so that sum is the softmax's and two passes
+ * suffice; fp16/bf16 round x - m to the storage type first, so a second pass
+ * sums exp(rnd(x - m)) against the final max (the first pass's sum is then
+ * the fused loss's). The last pass writes the outputs with the register
+ * path's expressions. Reads before the last use the default cache policy, so
+ * the later passes find the row in cache where they can. The labelled logit
+ * is taken from the first pass's registers by the thread holding it (the last
+ * pass may overwrite the row in place). */
+template <typename T, bool FUSED>
+__device__ __forceinline__ void smx_stream_vec(int n_rows, int n_cols, const T * X, T * out, const uint32_t * labels, float * loss) {
 	constexpr int U = 4;
+	constexpr int VEC = VecOf<T>::N;
+	constexpr bool ROUNDS = sizeof(T) < 4;
 	__shared__ float slots[32];
 	__shared__ float xlab_cell;
 	const int tid = threadIdx.x;
 	const int nt = blockDim.x;
-	const int nv = n_cols / 4;
-	const uint32_t row_bytes = (uint32_t) n_cols * 4u;
+	const int nv = n_cols / VEC;
+	const uint32_t row_bytes = (uint32_t) n_cols * (uint32_t) sizeof(T);
 	for (int row = blockIdx.x; row < n_rows; row += gridDim.x) {
 		const __amdgpu_buffer_rsrc_t rin = make_rsrc(X + (long) row * n_cols, row_bytes);
 		const __amdgpu_buffer_rsrc_t rout = make_rsrc(out + (long) row * n_cols, row_bytes);
 		const uint32_t lab = FUSED ? labels[row] : 0xffffffffu;
 		const bool lab_ok = FUSED && lab < (uint32_t) n_cols;
-		const int c_lab = lab_ok ? (int) (lab >> 2) : -1;
+		const int c_lab = lab_ok ? (int) (lab / VEC) : -1;
+		const int le = (int) (lab % VEC);
+		/* pass 1: max and the online sum of exp(x - m) */
 		float m = -__builtin_inff(), mref = 0.0f, s = 0.0f;
 		for (int base = 0; base < nv; base += nt * U) {
 			R16 v[U];
 #pragma unroll
 			for (int k = 0; k < U; k++) v[k] = buf_load16(rin, (uint32_t) (base + k * nt + tid) * 16u, 0);
-			float f[U][4];
+			float f[U][VEC];
 			float cm = m;
 #pragma unroll
 			for (int k = 0; k < U; k++) {
 				const int c = base + k * nt + tid;
-				unpack16<float>(v[k], f[k]);
+				unpack16<T>(v[k], f[k]);
 #pragma unroll
-				for (int e = 0; e < 4; e++) {
+				for (int e = 0; e < VEC; e++) {
 					if (c >= nv) f[k][e] = -__builtin_inff();
 					cm = fmaxf(cm, f[k][e]);
 				}
-				if (c == c_lab) xlab_cell = f[k][lab & 3u];
+				if (c == c_lab) xlab_cell = f[k][le];
 			}
 			const float mr = (cm == -__builtin_inff()) ? 0.0f : cm;
 			s *= __builtin_amdgcn_exp2f((mref - mr) * SMX_LOG2E);
 #pragma unroll
 			for (int k = 0; k < U; k++) {
 #pragma unroll
-				for (int e = 0; e < 4; e++) s += __builtin_amdgcn_exp2f((f[k][e] - mr) * SMX_LOG2E);
+				for (int e = 0; e < VEC; e++) s += __builtin_amdgcn_exp2f((f[k][e] - mr) * SMX_LOG2E);
 			}
 			mref = mr;
 			m = cm;
 		}
 		const float mx = block_max(m, slots);
-		float sr = s * __builtin_amdgcn_exp2f((mref - mx) * SMX_LOG2E);
-		float unused = 0.0f;
+		float sx = s * __builtin_amdgcn_exp2f((mref - mx) * SMX_LOG2E);
+		/* pass 2 (fp16/bf16): sd = sum exp(rnd(x - mx)) */
+		float sd = 0.0f;
+		if (ROUNDS) {
+			for (int base = 0; base < nv; base += nt * U) {
+				R16 v[U];
+#pragma unroll
+				for (int k = 0; k < U; k++) v[k] = buf_load16(rin, (uint32_t) (base + k * nt + tid) * 16u, 0);
+#pragma unroll
+				for (int k = 0; k < U; k++) {
+					if (base + k * nt + tid < nv) {
+						float f[VEC];
+						unpack16<T>(v[k], f);
+#pragma unroll
+						for (int e = 0; e < VEC; e++) sd += exp_fast(rnd_in<T>(f[e] - mx));
+					}
+				}
+			}
+		}
 		__syncthreads();   /* every wave has read the max cells */
-		block_sum2(sr, unused, slots);
-		const float nlog2s = -__builtin_amdgcn_logf(sr);
+		block_sum2(sx, sd, slots);
+		if (!ROUNDS) sd = sx;
+		const float nlog2s = -__builtin_amdgcn_logf(sd);
+		/* last pass: y = exp(rnd(x - mx)) / sd */
 		for (int base = 0; base < nv; base += nt * U) {
 			R16 v[U];
 #pragma unroll
@@ -554,15 +581,20 @@ __device__ __forceinline__ void smx_stream_f32(int n_rows, int n_cols, const flo
 #pragma unroll
 			for (int k = 0; k < U; k++) {
 				const int c = base + k * nt + tid;
-				float f[4];
-				unpack16<float>(v[k], f);
+				float f[VEC];
+				unpack16<T>(v[k], f);
 #pragma unroll
-				for (int e = 0; e < 4; e++) f[e] = __builtin_amdgcn_exp2f(fmaf(f[e] - mx, SMX_LOG2E, nlog2s));
-				if (c == c_lab) f[lab & 3u] -= 1.0f;
-				buf_store16_nt(rout, (uint32_t) c * 16u, 0, pack16<float>(f));
+				for (int e = 0; e < VEC; e++) f[e] = __builtin_amdgcn_exp2f(fmaf(rnd_in<T>(f[e] - mx), SMX_LOG2E, nlog2s));
+				R16 o = pack16<T>(f);
+				if (c == c_lab) {   /* the label element: rnd(y) - 1 */
+					unpack16<T>(o, f);
+					f[le] -= 1.0f;
+					o = pack16<T>(f);
+				}
+				buf_store16_nt(rout, (uint32_t) c * 16u, 0, o);
 			}
 		}
-		if (FUSED && tid == 0 && loss) loss[row] = lab_ok ? (logf(sr) + mx - xlab_cell) : __builtin_nanf("");
+		if (FUSED && tid == 0 && loss) loss[row] = lab_ok ? (logf(sx) + mx - xlab_cell) : __builtin_nanf("");
 		__syncthreads();   /* the cells are rewritten for the next row */
 	}
 }
@@ -573,8 +605,8 @@ __device__ __forceinline__ void smx(int n_rows, int n_cols, const T * X, TO * ou
 	const bool vec_ok = (n_cols % VEC == 0) && aligned16(X) && aligned16(out) && blockDim.x == SMX_THREADS
 						&& ((n_cols / VEC + SMX_THREADS - 1) / SMX_THREADS) <= SMX_MAXCH;
 	if (vec_ok) smx_regs<T, TO, FUSED>(n_rows, n_cols, X, out, labels, loss);
-	else if (sizeof(T) == 4 && sizeof(TO) == 4 && n_cols % 4 == 0 && aligned16(X) && aligned16(out) && blockDim.x == SMX_THREADS)
-		smx_stream_f32<FUSED>(n_rows, n_cols, reinterpret_cast<const float *>(X), reinterpret_cast<float *>(out), labels, loss);
+	else if (sizeof(TO) == sizeof(T) && n_cols % VEC == 0 && aligned16(X) && aligned16(out) && blockDim.x == SMX_THREADS)
+		smx_stream_vec<T, FUSED>(n_rows, n_cols, X, reinterpret_cast<T *>(out), labels, loss);
 	else smx_stream<T, TO, FUSED>(n_rows, n_cols, X, out, labels, loss);
 }
 

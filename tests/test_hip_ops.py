@@ -586,7 +586,7 @@ def special_logits(dt, shape, seed):
 # more rows than workgroups (each walks 2-3 rows with the next row, its label
 # and labelled logit in flight); 32000 and 24576 + 8 columns leave a partial
 # last chunk, 128256 is the Llama-3 vocabulary
-MANY_ROWS = [(700, 32000), (600, 24584), (300, 128256)]
+MANY_ROWS = [(700, 32000), (600, 24584), (300, 128256), (300, 151936)]   # 151936: half-precision rows past the register path
 MANY_ROWS += [(_ri(257, 700), 8 * _ri(125, 16032))]
 
 
