@@ -75,7 +75,9 @@ static void rms_rowwise(Hip_Launch_Config * c, Dataflow_Handle * h, Hip_Function
 	const int slots = MY_MAX(1, 256 / tpr);
 	const unsigned block = (unsigned) (slots * tpr);
 	const unsigned lds = (unsigned) (RMS_CELLS_PER_SLOT * slots * sizeof(float));
-	const long groups_per_cu = MY_CEIL(rms_slots_per_cu(n_cols, elem, arrays), (long) slots);
+	/* the element path (nv == 0) walks its rows with plain loads and keeps no
+	 * row in flight ahead, so it needs many rows per CU to hide latency */
+	const long groups_per_cu = (nv == 0) ? RMS_STREAM_GROUPS_PER_CU : MY_CEIL(rms_slots_per_cu(n_cols, elem, arrays), (long) slots);
 	long grid = MY_MIN((long) MY_CEIL(n_rows, slots), (long) dev(h)->cu_count * groups_per_cu);
 	grid = MY_MIN(grid, resident_groups(h, f, (int) block, lds));
 	set_1d(c, (unsigned) grid, block, lds);

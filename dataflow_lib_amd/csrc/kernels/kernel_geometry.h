@@ -16,6 +16,8 @@
 #define RMS_CH 2
 #define RMS_MAX_TPR 1024
 #define RMS_STREAM_TPR 256
+/* element-path workgroups (one 256-thread row slot each) per CU, at most */
+#define RMS_STREAM_GROUPS_PER_CU 8
 /* LDS floats per row slot for the row reductions: [2 parities][32] */
 #define RMS_CELLS_PER_SLOT 64
 /* launch target: bytes of row loads outstanding per CU (each row slot keeps

@@ -298,8 +298,23 @@ __device__ __forceinline__ void rms_stream(const RmsArgs & a, float * lds) {
 		const T * g = reinterpret_cast<const T *>(a.dY) + off;
 		T * yd = reinterpret_cast<T *>(a.Y_or_dX) + off;
 		if (MODE == RMS_FWD) {
+			/* rows too long for the vector path but 16-byte aligned: 16-byte
+			 * chunks; the second loop re-reads the row (from cache where it
+			 * still is) */
+			constexpr int V = VecOf<T>::N;
+			const bool vec = (n_cols % V) == 0 && aligned16(a.X) && aligned16(a.Y_or_dX) && aligned16(W);
+			const int nv = n_cols / V;
 			float ss = 0.0f, sw = 0.0f;
-			if (live) {
+			if (live && vec) {
+				for (int c = tr; c < nv; c += tpr) {
+					float xf[V], wf[V];
+					unpack16<T>(reinterpret_cast<const R16 *>(x)[c], xf);
+					unpack16<T>(reinterpret_cast<const R16 *>(W)[c], wf);
+#pragma unroll
+					for (int e = 0; e < V; e++) { sw = fmaf(xf[e], wf[e], sw); ss = fmaf(xf[e], xf[e], ss); }
+				}
+			}
+			else if (live) {
 				for (int j = tr; j < n_cols; j += tpr) {
 					const float xf = to_f(x[j]);
 					sw = fmaf(xf, to_f(W[j]), sw);
@@ -314,7 +329,19 @@ __device__ __forceinline__ void rms_stream(const RmsArgs & a, float * lds) {
 					if (a.ws_out) a.ws_out[row] = sw;
 					if (a.rs_out) a.rs_out[row] = r;
 				}
-				for (int j = tr; j < n_cols; j += tpr) yd[j] = from_f<T>((to_f(x[j]) * r) * to_f(W[j]));
+				if (vec) {
+					for (int c = tr; c < nv; c += tpr) {
+						float xf[V], wf[V];
+						unpack16<T>(ld16_nt(reinterpret_cast<const R16 *>(x) + c), xf);
+						unpack16<T>(reinterpret_cast<const R16 *>(W)[c], wf);
+#pragma unroll
+						for (int e = 0; e < V; e++) xf[e] = (xf[e] * r) * wf[e];
+						st16_nt(reinterpret_cast<R16 *>(yd) + c, pack16<T>(xf));
+					}
+				}
+				else {
+					for (int j = tr; j < n_cols; j += tpr) yd[j] = from_f<T>((to_f(x[j]) * r) * to_f(W[j]));
+				}
 			}
 		}
 		else if (MODE == RMS_BWD_X) {
