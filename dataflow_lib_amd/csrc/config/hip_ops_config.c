@@ -108,7 +108,7 @@ static int rms_dw_config(Hip_Launch_Config * c, Dataflow_Handle * h, Hip_Functio
 		set_1d(c, 0, 1, 0);
 		return 0;
 	}
-	const int tpr = rms_tpr_for(nv);
+	const int tpr = (nv > 0) ? rms_tpr_for(nv) : rms_stream_tpr(1, n_cols);
 	const long max_lds = f->function_config.func_max_smem > 0 ? f->function_config.func_max_smem : dev(h)->max_smem_per_block;
 	/* one workgroup per CU holding the CU's row slots (one dW partial row per
 	 * workgroup) */

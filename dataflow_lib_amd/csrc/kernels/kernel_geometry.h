@@ -81,6 +81,15 @@ GEOM_FN int rms_vec_chunks(int n_cols, int elem_bytes, unsigned long long ptr_or
 	return nv;
 }
 
+/* element path: threads per row slot. The dW modes (whose slots each keep an
+ * n_cols-float partial row in LDS, so that only one slot fits per workgroup
+ * once rows are long) use one slot of RMS_MAX_TPR threads from
+ * RMS_STREAM_WIDE_COLS columns on */
+#define RMS_STREAM_WIDE_COLS 4096
+GEOM_FN int rms_stream_tpr(int dw_mode, int n_cols) {
+	return (dw_mode && n_cols >= RMS_STREAM_WIDE_COLS) ? RMS_MAX_TPR : RMS_STREAM_TPR;
+}
+
 GEOM_FN int rms_tpr_for(int nv) {
 	if (nv == 0) return RMS_STREAM_TPR;
 	const int t = (nv + RMS_CH - 1) / RMS_CH;

@@ -275,7 +275,7 @@ __device__ __forceinline__ void rms_vector(const RmsArgs & a, int nv, float * ld
 /* element path: any alignment / row length; TPR = 256 */
 template <typename T, typename TW, int MODE>
 __device__ __forceinline__ void rms_stream(const RmsArgs & a, float * lds) {
-	const int tpr = RMS_STREAM_TPR;
+	const int tpr = rms_stream_tpr(MODE == RMS_BWD_W || MODE == RMS_BWD, a.n_cols);
 	const int slots = blockDim.x / tpr;
 	const int slot = threadIdx.x / tpr;
 	const int tr = threadIdx.x % tpr;
@@ -356,9 +356,27 @@ __device__ __forceinline__ void rms_stream(const RmsArgs & a, float * lds) {
 		}
 		else {
 			const float r = live ? a.rs_in[row] : 0.0f;
+			/* 16-byte chunks when every row operand is aligned */
+			constexpr int V = VecOf<T>::N;
+			const bool vec = (n_cols % V) == 0 && aligned16(a.X) && aligned16(a.dY) &&
+							 (MODE == RMS_BWD_W || (aligned16(a.Y_or_dX) && aligned16(W)));
+			const int nv = n_cols / V;
+			const R16 * xv = reinterpret_cast<const R16 *>(x);
+			const R16 * gv = reinterpret_cast<const R16 *>(g);
 			if (MODE == RMS_BWD) {
+				const R16 * wv = reinterpret_cast<const R16 *>(W);
 				float dot = 0.0f;
-				if (live) {
+				if (live && vec) {
+					for (int c = tr; c < nv; c += tpr) {
+						float xf[V], gf[V], wf[V];
+						unpack16<T>(xv[c], xf);
+						unpack16<T>(gv[c], gf);
+						unpack16<T>(wv[c], wf);
+#pragma unroll
+						for (int e = 0; e < V; e++) dot = fmaf(gf[e] * wf[e], xf[e], dot);
+					}
+				}
+				else if (live) {
 					for (int j = tr; j < n_cols; j += tpr) dot = fmaf(to_f(g[j]) * to_f(W[j]), to_f(x[j]), dot);
 				}
 				float unused = 0.0f;
@@ -366,14 +384,44 @@ __device__ __forceinline__ void rms_stream(const RmsArgs & a, float * lds) {
 				parity ^= 1;
 				if (live) {
 					const float coef = ((r * r * r) * dot) / (float) n_cols;
-					for (int j = tr; j < n_cols; j += tpr) {
-						const float gw = to_f(g[j]) * to_f(W[j]);
-						yd[j] = from_f<T>(to_f(yd[j]) + (r * gw - to_f(x[j]) * coef));
+					if (vec) {
+						R16 * dv = reinterpret_cast<R16 *>(yd);
+						for (int c = tr; c < nv; c += tpr) {
+							float xf[V], gf[V], wf[V], df[V];
+							unpack16<T>(xv[c], xf);
+							unpack16<T>(gv[c], gf);
+							unpack16<T>(wv[c], wf);
+							unpack16<T>(dv[c], df);
+#pragma unroll
+							for (int e = 0; e < V; e++) {
+								const float gw = gf[e] * wf[e];
+								df[e] = df[e] + (r * gw - xf[e] * coef);
+								mycol[c * V + e] = fmaf(gf[e] * xf[e], r, mycol[c * V + e]);
+							}
+							dv[c] = pack16<T>(df);
+						}
+					}
+					else {
+						for (int j = tr; j < n_cols; j += tpr) {
+							const float gw = to_f(g[j]) * to_f(W[j]);
+							yd[j] = from_f<T>(to_f(yd[j]) + (r * gw - to_f(x[j]) * coef));
+						}
 					}
 				}
 			}
-			if (live) {
-				for (int j = tr; j < n_cols; j += tpr) mycol[j] = fmaf(to_f(g[j]) * to_f(x[j]), r, mycol[j]);
+			if (live && !(MODE == RMS_BWD && vec)) {   /* (the fused vector loop above already accumulated dW) */
+				if (vec) {
+					for (int c = tr; c < nv; c += tpr) {
+						float xf[V], gf[V];
+						unpack16<T>(xv[c], xf);
+						unpack16<T>(gv[c], gf);
+#pragma unroll
+						for (int e = 0; e < V; e++) mycol[c * V + e] = fmaf(gf[e] * xf[e], r, mycol[c * V + e]);
+					}
+				}
+				else {
+					for (int j = tr; j < n_cols; j += tpr) mycol[j] = fmaf(to_f(g[j]) * to_f(x[j]), r, mycol[j]);
+				}
 			}
 		}
 	}

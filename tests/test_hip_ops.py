@@ -81,7 +81,7 @@ def _ri(lo, hi):
 
 # (8192, 4096) is the Llama-3-8B token batch: every workgroup walks several
 # rows there, with the next row's loads in flight across each row's reduction
-RMS_SHAPES = [(16, 4096), (64, 4096), (7, 8192), (33, 1000), (5, 8), (3, 20000), (8192, 4096)]
+RMS_SHAPES = [(16, 4096), (64, 4096), (7, 8192), (33, 1000), (5, 8), (3, 20000), (8192, 4096), (5, 4099)]   # 4099: wide ragged rows
 RMS_SHAPES += [(_ri(1, 2000), 8 * _ri(1, 1024)), (_ri(1, 300), _ri(1, 9000)), (_ri(500, 3000), 8 * _ri(200, 700))]
 
 
