@@ -349,8 +349,27 @@ __device__ __forceinline__ void rms_stream(const RmsArgs & a, float * lds) {
 				const float r = a.rs_in[row];
 				const float ws = a.ws_in[row];
 				const float r3 = r * r * r;
-				for (int j = tr; j < n_cols; j += tpr) {
-					yd[j] = from_f<T>(bwd_x_elem<T>(to_f(W[j]), to_f(x[j]), to_f(g[j]), to_f(yd[j]), r, r3, ws, n_cols));
+				constexpr int V = VecOf<T>::N;
+				if ((n_cols % V) == 0 && aligned16(a.X) && aligned16(a.dY) && aligned16(a.Y_or_dX) && aligned16(W)) {
+					const R16 * wv = reinterpret_cast<const R16 *>(W);
+					const R16 * xv = reinterpret_cast<const R16 *>(x);
+					const R16 * gv = reinterpret_cast<const R16 *>(g);
+					R16 * dv = reinterpret_cast<R16 *>(yd);
+					for (int c = tr; c < n_cols / V; c += tpr) {
+						float wf[V], xf[V], gf[V], df[V];
+						unpack16<T>(wv[c], wf);
+						unpack16<T>(xv[c], xf);
+						unpack16<T>(gv[c], gf);
+						unpack16<T>(dv[c], df);
+#pragma unroll
+						for (int e = 0; e < V; e++) df[e] = bwd_x_elem<T>(wf[e], xf[e], gf[e], df[e], r, r3, ws, n_cols);
+						dv[c] = pack16<T>(df);
+					}
+				}
+				else {
+					for (int j = tr; j < n_cols; j += tpr) {
+						yd[j] = from_f<T>(bwd_x_elem<T>(to_f(W[j]), to_f(x[j]), to_f(g[j]), to_f(yd[j]), r, r3, ws, n_cols));
+					}
 				}
 			}
 		}
