@@ -288,6 +288,11 @@ __device__ __forceinline__ void rms_stream(const RmsArgs & a, float * lds) {
 	float * mycol = colbuf + (long) slot * n_cols;
 	if (MODE == RMS_BWD_W || MODE == RMS_BWD) {
 		for (int j = tr; j < n_cols; j += tpr) mycol[j] = 0.0f;
+		/* the zeroing maps elements to threads one by one, the 16-byte update
+		 * loops map 16-byte chunks: without this barrier a thread can clear an
+		 * element another thread has already accumulated (RMS_BWD_W reads r
+		 * from the saved statistics, so no row reduction orders them) */
+		__syncthreads();
 	}
 	int parity = 0;
 	for (int base_row = blockIdx.x * slots; base_row < a.n_rows; base_row += gridDim.x * slots) {
