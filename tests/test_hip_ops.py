@@ -216,6 +216,31 @@ def test_rms_norm_bwd_repeat_is_deterministic(hdl):
         assert np.array_equal(a, outs[0][0]) and np.array_equal(b.view(np.uint32), outs[0][1].view(np.uint32))
 
 
+@pytest.mark.parametrize("dt", [FP32, BF16], ids=dt_id)
+@pytest.mark.parametrize("shape", [(3, 20000), (64, 24576), (5, 36000)], ids=lambda s: "%dx%d" % s)
+def test_rms_norm_bwd_w_wide_rows_repeat(hdl, dt, shape):
+    """Rows too wide for the register path accumulate dW in an LDS row that is
+    zeroed element by element and updated in 16-byte chunks by other threads;
+    every launch must see the zeroing finished first. Eight launches, each
+    checked against the oracle and bit-equal to the first."""
+    from dataflow_lib_amd import api
+    n_rows, n_cols = shape
+    X, W, ws, rs, dY, _ = rms_bwd_inputs(dt, n_rows, n_cols, seed=43)
+    dW = to_storage(normal(22, (n_cols,), std=0.1), dt)
+    pre, absum = np.empty(n_cols), np.empty(n_cols)
+    assert oracle().oracle_rms_norm_bwd_w(dt, dt, n_rows, n_cols, ptr(rs), ptr(X), ptr(dY), ptr(dW), ptr(pre), ptr(absum)) == 0
+    outs = []
+    with Dev(hdl) as d:
+        prs, px, pdy = d.put(rs), d.put(X), d.put(dY)
+        for _ in range(8):
+            pdw = d.put(dW)
+            assert api.submit_rms_norm_bwd_w(hdl, 0, dt, dt, n_rows, n_cols, 1e-5, prs, px, pdy, pdw) == 0
+            outs.append(d.get(pdw, (n_cols,), NP_STORAGE[dt]))
+    for k, out in enumerate(outs):
+        check_rounded(out, dt, pre, floor=1e-6 * absum, what="rms_norm_bwd_w dW, launch %d" % k)
+        assert np.array_equal(out, outs[0])
+
+
 def test_dw_ops_on_two_streams_match_one_stream(hdl):
     """The dW ops keep their partial rows in the code object's scratch; the
     handle orders them across streams, so a large launch on stream 0 followed
