@@ -241,6 +241,37 @@ def test_rms_norm_bwd_w_wide_rows_repeat(hdl, dt, shape):
         assert np.array_equal(out, outs[0])
 
 
+def test_empty_inputs_launch_nothing(hdl):
+    """Zero rows (and zero SwiGLU columns, zero RoPE/scatter elements): every
+    op returns 0 and leaves every buffer it was given untouched — including
+    dW for the two-pass ops and the mean loss, which has no rows to average."""
+    from dataflow_lib_amd import api
+    dt, C, V = BF16, 4096, 128256
+    sentinel = np.full(1 << 20, 0x5A, np.uint8)
+    with Dev(hdl) as d:
+        bufs = [d.put(sentinel) for _ in range(8)]
+        p0, p1, p2, p3, p4, p5, p6, p7 = bufs
+        calls = [
+            ("rms_norm", lambda: api.submit_rms_norm(hdl, 0, dt, 0, C, 1e-5, p0, p1, p2, p3, p4)),
+            ("rms_norm_bwd_x", lambda: api.submit_rms_norm_bwd_x(hdl, 0, dt, dt, 0, C, 1e-5, p0, p1, p2, p3, p4, p5)),
+            ("rms_norm_bwd_w", lambda: api.submit_rms_norm_bwd_w(hdl, 0, dt, dt, 0, C, 1e-5, p0, p1, p2, p3)),
+            ("rms_norm_bwd", lambda: api.submit_rms_norm_bwd(hdl, 0, dt, dt, 0, C, 1e-5, p0, p1, p2, p3, p4, p5)),
+            ("rope", lambda: api.submit_rope(hdl, 0, dt, 0, C, 128, 8, 500000, p0, p1, p2)),
+            ("rope_bwd_x", lambda: api.submit_rope_bwd_x(hdl, 0, dt, 0, C, 128, 8, 500000, p0, p1, p2)),
+            ("swiglu rows", lambda: api.submit_swiglu(hdl, 0, dt, 0, 14336, p0, p1, p2)),
+            ("swiglu cols", lambda: api.submit_swiglu(hdl, 0, dt, 5, 0, p0, p1, p2)),
+            ("swiglu_bwd_x", lambda: api.submit_swiglu_bwd_x(hdl, 0, dt, dt, 0, 14336, p0, p1, p2, p3, p4)),
+            ("softmax", lambda: api.submit_softmax(hdl, 0, dt, dt, 0, V, p0, p1)),
+            ("cross_entropy_loss", lambda: api.submit_cross_entropy_loss(hdl, 0, dt, 0, V, p0, p1)),
+            ("softmax_cross_entropy_loss", lambda: api.submit_softmax_cross_entropy_loss(hdl, 0, dt, 0, V, p0, p1, p2, p3)),
+            ("copy_to_seq_context", lambda: api.submit_copy_to_seq_context(hdl, 0, dt, 0, 0, 1024, p0, p1, p2, p3, p4)),
+        ]
+        for name, call in calls:
+            assert call() == 0, name
+            for k, p in enumerate(bufs):
+                assert np.array_equal(d.get(p, sentinel.shape, np.uint8), sentinel), "%s wrote buffer %d" % (name, k)
+
+
 def test_dw_ops_on_two_streams_match_one_stream(hdl):
     """The dW ops keep their partial rows in the code object's scratch; the
     handle orders them across streams, so a large launch on stream 0 followed
