@@ -15,7 +15,10 @@ Inputs are resident in HBM before timing. Each op rotates through enough
 buffer sets that its working set per rotation is >= 1 GiB, so the 256 MB
 Infinity Cache cannot serve repeats. The K timed steps run back to back
 between two events on the launch stream (an event between kernels would add
-several microseconds of stream time to every op); `value` = sum of per-op
+several microseconds of stream time to every op). K defaults to 100: the
+timed region starts after a synchronize, and the first launches into the idle
+GPU cost about 0.5 ms once, which at K = 20 added ~25 us to every step (847
+against 821 us of per-op time) and at K = 100 ~8 us; `value` = sum of per-op
 algorithmic bytes / measured step time. Per-op time = the average launch
 duration of K back-to-back launches of that op alone (rotating its sets),
 between two events on the launch stream. Timed as extras, outside `value`: the
@@ -502,7 +505,7 @@ def load_traffic(name):
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
-    ap.add_argument("--steps", type=int, default=20)
+    ap.add_argument("--steps", type=int, default=100)
     ap.add_argument("--warmup", type=int, default=3)
     ap.add_argument("--no-extras", action="store_true")
     ap.add_argument("--no-head", action="store_true", help="skip the transformer-head (GEMM) line")
