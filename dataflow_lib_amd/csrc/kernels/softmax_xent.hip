@@ -209,11 +209,13 @@ typedef __attribute__((address_space(3))) void * lds_ptr_t;
  * this row's max pass and lands while it computes: its first SMX_PF chunks go
  * straight into LDS (16-byte buffer loads with the LDS bit), the others into
  * registers, and the fused op's next label into an LDS cell (a 4-byte LDS
- * load per wave; the word holding the labelled logit follows the same way, for
- * thread 0, once the label is known). Each wave prefetches into and reads from
- * its own LDS slice only, so no workgroup barrier guards the buffer, and the
- * reductions' barriers wait for LDS only: the one wait for memory in a row is
- * the one before the output pass. */
+ * load per wave). The labelled logit is copied out of the registers of the
+ * thread holding it during the max pass, before the row is overwritten in
+ * place, and reaches thread 0 (which writes the loss) through an LDS cell.
+ * Each wave prefetches into and reads from its own LDS slice only, so no
+ * workgroup barrier guards the buffer, and the reductions' barriers wait for
+ * LDS only: the one wait for memory in a row is the one before the output
+ * pass. */
 template <typename T, typename TO, bool FUSED>
 __device__ __forceinline__ void smx_regs(int n_rows, int n_cols, const T * X, TO * out, const uint32_t * labels, float * loss) {
 	constexpr int VEC = VecOf<T>::N;
@@ -234,7 +236,11 @@ __device__ __forceinline__ void smx_regs(int n_rows, int n_cols, const T * X, TO
 	 * own wait for memory covers it (a load issued by one wave is not waited
 	 * for by the others) */
 	__shared__ uint32_t labcell[SMX_WAVES];
-	__shared__ uint32_t xlabcell[1];          /* the 4-byte word holding the labelled logit (thread 0) */
+	/* the labelled logit, written by the thread holding it during the max
+	 * pass and read by thread 0 after the sum reduction's barrier; two cells
+	 * by row parity, since the next row's writer can run ahead of thread 0's
+	 * read by up to one row (never two: the next row's sum barrier comes first) */
+	__shared__ float xlab_cell[2];
 	const int tid = threadIdx.x;
 	constexpr int nt = SMX_THREADS;          /* the launch guarantees blockDim.x == SMX_THREADS */
 	static_assert((nt & (nt - 1)) == 0, "power-of-two workgroup");
@@ -254,20 +260,13 @@ __device__ __forceinline__ void smx_regs(int n_rows, int n_cols, const T * X, TO
 		if (FUSED && lane == 0)
 			__builtin_amdgcn_raw_ptr_buffer_load_lds(rlab, (lds_ptr_t) &labcell[wave], 4, 0u, (uint32_t) r * 4u, 0, 0);
 	};
-	/* the word of row r holding element j (rows are 16-byte aligned), for
-	 * thread 0, which writes the loss */
-	auto fetch_logit_word = [&](int r, uint32_t j) {
-		if (FUSED && tid == 0) {
-			const __amdgpu_buffer_rsrc_t rr = make_rsrc(X + (long) r * n_cols, row_bytes);
-			__builtin_amdgcn_raw_ptr_buffer_load_lds(rr, (lds_ptr_t) xlabcell, 4, 0u, (j * (uint32_t) sizeof(T)) & ~3u, 0, 0);
-		}
-	};
 
 	/* chunks SMX_PF .. SMX_PF + RP - 1 of the next row are loaded a row ahead
 	 * into VGPRs; fp32 rows keep those registers for temporaries and load the
 	 * chunks past SMX_PF + RP at the top of their own row */
 	constexpr int RP = sizeof(T) < 4 ? SMX_MAXCH - SMX_PF : 0;
 	int row = blockIdx.x;
+	int par = 0;
 	R16 xr[SMX_MAXCH];
 	R16 nx[RP > 0 ? RP : 1];
 	/* prologue: this workgroup's first row, LDS part and register part */
@@ -303,10 +302,7 @@ __device__ __forceinline__ void smx_regs(int n_rows, int n_cols, const T * X, TO
 		/* the next row (requested during the max pass) and its label */
 		const int next = row + gridDim.x;
 		const bool has_next = next < n_rows;
-		/* the labelled logit's word: landed by the wait before the output pass,
-		 * which is also before this row is overwritten */
 		const bool lab_ok = FUSED && lab < (uint32_t) n_cols;
-		if (lab_ok) fetch_logit_word(row, lab);
 		const __amdgpu_buffer_rsrc_t rn = make_rsrc(X + (long) next * n_cols, has_next ? row_bytes : 0u);
 		auto issue_next = [&](int c) {
 			if (has_next && c < nch) {
@@ -359,6 +355,15 @@ __device__ __forceinline__ void smx_regs(int n_rows, int n_cols, const T * X, TO
 				float cm = m;
 #pragma unroll
 				for (int e = 0; e < VEC; e++) cm = __builtin_elementwise_maximum(cm, f[e]);
+				/* the raw labelled logit, for the loss (a workgroup-uniform
+				 * chunk test, then one thread) */
+				if (FUSED && c == c_lab && tid == t_lab) {
+					float xl = f[0];
+#pragma unroll
+					for (int e = 1; e < VEC; e++)
+						if (e == le) xl = f[e];
+					xlab_cell[par] = xl;
+				}
 				if (SX) {
 					const float mr = (cm == -__builtin_inff()) ? 0.0f : cm;
 					so *= __builtin_amdgcn_exp2f((mref - mr) * SMX_LOG2E);
@@ -436,15 +441,8 @@ __device__ __forceinline__ void smx_regs(int n_rows, int n_cols, const T * X, TO
 				buf_store16_nt(rout, voff, c * cstride, o);
 			}
 		}
-		if (FUSED && tid == 0 && loss) {
-			float x_lab = 0.0f;
-			if (lab_ok) {
-				float f[W::N];
-				W::unpack(xlabcell[0], f);
-				x_lab = (W::N == 2 && (lab & 1)) ? f[W::N - 1] : f[0];
-			}
-			loss[row] = lab_ok ? (logf(sx) + m - x_lab) : __builtin_nanf("");
-		}
+		if (FUSED && tid == 0 && loss) loss[row] = lab_ok ? (logf(sx) + m - xlab_cell[par]) : __builtin_nanf("");
+		par ^= 1;
 	}
 	WAIT_VMEM_ALL();
 }
