@@ -20,7 +20,7 @@
 #define HIP_CHECK_RET(call, ret, ...) do { \
 		hipError_t _e = (call); \
 		if (_e != hipSuccess) { \
-			fprintf(stderr, "Error: %s failed: %s. ", #call, hipGetErrorString(_e)); \
+			fprintf(stderr, "hip backend: %s returned %s; ", #call, hipGetErrorString(_e)); \
 			fprintf(stderr, __VA_ARGS__); \
 			fprintf(stderr, "\n"); \
 			return ret; \
@@ -38,7 +38,7 @@ static int resolve_stream(Dataflow_Handle * h, int stream_id, hipStream_t * out,
 		return 0;
 	}
 	if (stream_id < 0 || stream_id >= h->num_streams) {
-		fprintf(stderr, "Error: cannot use stream id %d for %s, device has %d streams. Null stream specified by -1...\n",
+		fprintf(stderr, "hip backend: stream id %d (for %s) is out of range: the handle has %d streams, and -1 names the null stream\n",
 				stream_id, what, h->num_streams);
 		return -1;
 	}
@@ -51,26 +51,26 @@ static int resolve_stream(Dataflow_Handle * h, int stream_id, hipStream_t * out,
 static int hip_register_native_code(Dataflow_Handle * dataflow_handle, char * native_code_filename, char * native_code_config_lib_filename,
 									int num_funcs, Op_Skeleton * func_op_skeletons, char ** func_symbols, char ** func_set_launch_symbols, char ** func_init_symbols) {
 	if (dataflow_handle->num_native_function_libs >= MAX_NATIVE_FUNCTION_LIBS) {
-		fprintf(stderr, "Error: cannot register more than %d native function libs...\n", MAX_NATIVE_FUNCTION_LIBS);
+		fprintf(stderr, "hip backend: the handle already holds the maximum of %d native code objects\n", MAX_NATIVE_FUNCTION_LIBS);
 		return -1;
 	}
 	HIP_CHECK_RET(hipSetDevice(dataflow_handle->device_id), -1, "device %d", dataflow_handle->device_id);
 
 	hipModule_t * module = (hipModule_t *) malloc(sizeof(hipModule_t));
 	if (!module) {
-		fprintf(stderr, "Error: malloc failed to allocate space for module container...\n");
+		fprintf(stderr, "hip backend: out of host memory for a module record\n");
 		return -1;
 	}
 	hipError_t err = hipModuleLoad(module, native_code_filename);
 	if (err != hipSuccess) {
-		fprintf(stderr, "Error: unable to load function lib from path: %s (%s)...\n", native_code_filename, hipGetErrorString(err));
+		fprintf(stderr, "hip backend: hipModuleLoad could not load the code object %s (%s)\n", native_code_filename, hipGetErrorString(err));
 		free(module);
 		return -1;
 	}
 
 	void * config_lib = dlopen(native_code_config_lib_filename, RTLD_LAZY | RTLD_LOCAL);
 	if (!config_lib) {
-		fprintf(stderr, "Error: could not load function config shared lib with dlopen() from path: %s (%s)\n",
+		fprintf(stderr, "hip backend: dlopen could not open the launch-config library %s (%s)\n",
 				native_code_config_lib_filename, dlerror());
 		hipModuleUnload(*module);
 		free(module);
@@ -84,7 +84,7 @@ static int hip_register_native_code(Dataflow_Handle * dataflow_handle, char * na
 			continue;
 		}
 		if (!func_set_launch_symbols[i]) {
-			fprintf(stderr, "Error: set launch symbol not set for native function %s, but is required for native functions..\n", sym);
+			fprintf(stderr, "hip backend: native function %s has no launch-config symbol; skipped\n", sym);
 			continue;
 		}
 
@@ -94,7 +94,7 @@ static int hip_register_native_code(Dataflow_Handle * dataflow_handle, char * na
 
 		err = hipModuleGetFunction(&f.function_handle, *module, sym);
 		if (err != hipSuccess) {
-			fprintf(stderr, "Error: failed to load function #%d with name %s from function lib (%s)...\n", i, sym, hipGetErrorString(err));
+			fprintf(stderr, "hip backend: kernel #%d (%s) is not in the code object (%s); skipped\n", i, sym, hipGetErrorString(err));
 			continue;
 		}
 
@@ -105,23 +105,9 @@ static int hip_register_native_code(Dataflow_Handle * dataflow_handle, char * na
 		f.function_config.func_max_threads_per_block = MY_MIN(max_threads, HIP_DEV_UPPER_BOUND_MAX_THREADS_ALL_FUNC);
 		f.function_config.func_max_smem = ((Hip_Device_Info *) dataflow_handle->device_info)->max_smem_per_block;
 
-		if (func_init_symbols && func_init_symbols[i]) {
-			Hip_Set_Func_Attribute init_fn = (Hip_Set_Func_Attribute) dlsym(config_lib, func_init_symbols[i]);
-			if (!init_fn) {
-				fprintf(stderr, "Error: failed to load symbol to initialize function #%d with name %s and attribute setting function as %s...\n",
-						i, sym, func_init_symbols[i]);
-				continue;
-			}
-			if (init_fn(dataflow_handle, &f)) {
-				fprintf(stderr, "Error: failed to set function attributes for function #%d with name %s and attribute setting function as %s\n",
-						i, sym, func_init_symbols[i]);
-				continue;
-			}
-		}
-
 		f.set_launch_config = (Hip_Set_Launch_Config) dlsym(config_lib, func_set_launch_symbols[i]);
 		if (!f.set_launch_config) {
-			fprintf(stderr, "Error: failed to get function pointer to launch config for function #%d with name %s and set_launch_config function name as %s\n",
+			fprintf(stderr, "hip backend: kernel #%d (%s): launch-config symbol %s is not in the launch-config library; skipped\n",
 					i, sym, func_set_launch_symbols[i]);
 			continue;
 		}
@@ -136,13 +122,13 @@ static int hip_register_native_code(Dataflow_Handle * dataflow_handle, char * na
 			size_t slen = strlen(suffix);
 			char finish_cfg[FUNC_SYMBOL_MAX_LEN + 32];
 			if (len <= slen || strcmp(func_set_launch_symbols[i] + len - slen, suffix) != 0) {
-				fprintf(stderr, "Error: launch symbol %s of two-pass function %s does not end in %s...\n", func_set_launch_symbols[i], sym, suffix);
+				fprintf(stderr, "hip backend: launch-config symbol %s of two-kernel function %s does not end in %s; skipped\n", func_set_launch_symbols[i], sym, suffix);
 				continue;
 			}
 			snprintf(finish_cfg, sizeof(finish_cfg), "%.*s_set_finish_launch_config", (int) (len - slen), func_set_launch_symbols[i]);
 			f.set_finish_launch_config = (Hip_Set_Launch_Config) dlsym(config_lib, finish_cfg);
 			if (!f.set_finish_launch_config) {
-				fprintf(stderr, "Error: function %s has a finish kernel but no %s in the config lib...\n", sym, finish_cfg);
+				fprintf(stderr, "hip backend: %s has a second kernel but the launch-config library lacks %s; skipped\n", sym, finish_cfg);
 				continue;
 			}
 			f.finish_function_handle = finish_fn;
@@ -156,15 +142,30 @@ static int hip_register_native_code(Dataflow_Handle * dataflow_handle, char * na
 		f.hip_external_func = NULL;
 		f.op_extra = NULL;
 
+		/* the init sees the whole record (skeleton and second kernel included) */
+		if (func_init_symbols && func_init_symbols[i]) {
+			Hip_Set_Func_Attribute init_fn = (Hip_Set_Func_Attribute) dlsym(config_lib, func_init_symbols[i]);
+			if (!init_fn) {
+				fprintf(stderr, "hip backend: kernel #%d (%s): init symbol %s is not in the launch-config library; skipped\n",
+						i, sym, func_init_symbols[i]);
+				continue;
+			}
+			if (init_fn(dataflow_handle, &f)) {
+				fprintf(stderr, "hip backend: kernel #%d (%s): init %s reported an error; skipped\n",
+						i, sym, func_init_symbols[i]);
+				continue;
+			}
+		}
+
 		if (insert_table(&dataflow_handle->op_table, f.op_skeleton.identifier.fingerprint, &f)) {
-			fprintf(stderr, "Error: failed to insert op for function #%d with name %s to op table...\n", i, sym);
+			fprintf(stderr, "hip backend: kernel #%d (%s) could not be added to the op table; skipped\n", i, sym);
 			continue;
 		}
 		added++;
 	}
 
 	if (added == 0) {
-		fprintf(stderr, "Error: no functions were added to op table...\n");
+		fprintf(stderr, "hip backend: none of the requested functions could be registered\n");
 		dlclose(config_lib);
 		hipModuleUnload(*module);
 		free(module);
@@ -180,7 +181,7 @@ static int hip_register_external_code(Dataflow_Handle * dataflow_handle, char * 
 									Op_Skeleton * func_op_skeletons, char ** func_symbols, char ** func_init_symbols) {
 	void * lib = dlopen(external_code_filename, RTLD_LAZY | RTLD_LOCAL);
 	if (!lib) {
-		fprintf(stderr, "Error: could not open external library with path: %s (%s)\n", external_code_filename, dlerror());
+		fprintf(stderr, "hip backend: dlopen could not open the external op library %s (%s)\n", external_code_filename, dlerror());
 		return -1;
 	}
 	int added = 0;
@@ -193,24 +194,24 @@ static int hip_register_external_code(Dataflow_Handle * dataflow_handle, char * 
 		memset(&f, 0, sizeof(f));
 		f.hip_external_func = (int (*)(Dataflow_Handle *, int, Op *, void *)) dlsym(lib, sym);
 		if (!f.hip_external_func) {
-			fprintf(stderr, "Error: could not obtain function symbol %s from external lib %s...\n", sym, external_code_filename);
+			fprintf(stderr, "hip backend: symbol %s is not in the external op library %s; skipped\n", sym, external_code_filename);
 			continue;
 		}
 		if (func_init_symbols && func_init_symbols[i]) {
 			External_Lib_Func_Init init_fn = (External_Lib_Func_Init) dlsym(lib, func_init_symbols[i]);
 			if (!init_fn) {
-				fprintf(stderr, "Error: could not get ref to initialization function %s, for external function %s\n", func_init_symbols[i], sym);
+				fprintf(stderr, "hip backend: init symbol %s of external function %s not found; skipped\n", func_init_symbols[i], sym);
 				continue;
 			}
 			if (init_fn(dataflow_handle, (void *) &f)) {
-				fprintf(stderr, "Error: initialization function %s, for external function %s returned an error...\n", func_init_symbols[i], sym);
+				fprintf(stderr, "hip backend: init %s of external function %s reported an error; skipped\n", func_init_symbols[i], sym);
 				continue;
 			}
 		}
 		memcpy(&f.op_skeleton, &func_op_skeletons[i], sizeof(Op_Skeleton));
 		f.is_native = false;
 		if (insert_table(&dataflow_handle->op_table, f.op_skeleton.identifier.fingerprint, &f)) {
-			fprintf(stderr, "Error: failed to insert op for function #%d with name %s to op table...\n", i, sym);
+			fprintf(stderr, "hip backend: kernel #%d (%s) could not be added to the op table; skipped\n", i, sym);
 			continue;
 		}
 		added++;
@@ -226,7 +227,7 @@ static int launch(hipFunction_t fn, Hip_Launch_Config * cfg, hipStream_t stream,
 											cfg->blockDimX, cfg->blockDimY, cfg->blockDimZ,
 											cfg->sharedMemBytes, stream, op->op_args, NULL);
 	if (err != hipSuccess) {
-		fprintf(stderr, "Error: unable to launch hip function: %s\n", hipGetErrorString(err));
+		fprintf(stderr, "hip backend: hipModuleLaunchKernel returned %s\n", hipGetErrorString(err));
 		return -1;
 	}
 	return 0;
@@ -250,7 +251,7 @@ static int hip_submit_op(Dataflow_Handle * dataflow_handle, Op * op, int stream_
 		Hip_Launch_Config cfg;
 		memset(&cfg, 0, sizeof(cfg));
 		if (f->set_launch_config(&cfg, dataflow_handle, f, op)) {
-			fprintf(stderr, "Error: failed to correctly set launch config for op with nickname %s...\n", nick);
+			fprintf(stderr, "hip backend: op %s: the launch configuration rejected these arguments\n", nick);
 			return -1;
 		}
 		/* a zero-sized grid means there is no work (e.g. zero rows) */
@@ -258,30 +259,32 @@ static int hip_submit_op(Dataflow_Handle * dataflow_handle, Op * op, int stream_
 			return 0;
 		}
 		Hip_Context * hc = (Hip_Context *) dataflow_handle->ctx;
-		if (f->finish_function_handle && hc->two_pass_stream != HIP_NO_STREAM && hc->two_pass_stream != stream_id) {
-			/* the previous two-pass op ran on another stream and shares the
-			 * module scratch: wait for that stream's queued work */
+		if (f->function_config.shares_module_scratch && hc->two_pass_stream != HIP_NO_STREAM && hc->two_pass_stream != stream_id) {
+			/* the previous op using the module scratch ran on another stream:
+			 * wait for that stream's queued work */
 			hipStream_t prev;
 			if (resolve_stream(dataflow_handle, hc->two_pass_stream, &prev, nick)) {
 				return -1;
 			}
-			HIP_CHECK_RET(hipEventRecord(hc->two_pass_event, prev), -1, "ordering op %s after the previous two-pass op", nick);
-			HIP_CHECK_RET(hipStreamWaitEvent(stream, hc->two_pass_event, 0), -1, "ordering op %s after the previous two-pass op", nick);
+			HIP_CHECK_RET(hipEventRecord(hc->two_pass_event, prev), -1, "ordering op %s after the previous scratch user", nick);
+			HIP_CHECK_RET(hipStreamWaitEvent(stream, hc->two_pass_event, 0), -1, "ordering op %s after the previous scratch user", nick);
 		}
 		if (launch(f->function_handle, &cfg, stream, op)) {
-			fprintf(stderr, "Error: failed to launch kernel for op with nickname %s...\n", nick);
+			fprintf(stderr, "hip backend: op %s: kernel launch failed\n", nick);
 			return -1;
 		}
-		if (f->finish_function_handle) {
+		if (f->function_config.shares_module_scratch) {
 			hc->two_pass_stream = stream_id;
+		}
+		if (f->finish_function_handle) {
 			Hip_Launch_Config fcfg;
 			memset(&fcfg, 0, sizeof(fcfg));
 			if (f->set_finish_launch_config(&fcfg, dataflow_handle, f, op)) {
-				fprintf(stderr, "Error: failed to set finish launch config for op with nickname %s...\n", nick);
+				fprintf(stderr, "hip backend: op %s: the second kernel's launch configuration rejected these arguments\n", nick);
 				return -1;
 			}
 			if (fcfg.gridDimX && fcfg.gridDimY && fcfg.gridDimZ && launch(f->finish_function_handle, &fcfg, stream, op)) {
-				fprintf(stderr, "Error: failed to launch finish kernel for op with nickname %s...\n", nick);
+				fprintf(stderr, "hip backend: op %s: second kernel launch failed\n", nick);
 				return -1;
 			}
 		}
@@ -289,11 +292,11 @@ static int hip_submit_op(Dataflow_Handle * dataflow_handle, Op * op, int stream_
 	}
 
 	if (!f->hip_external_func) {
-		fprintf(stderr, "Error: if op is not native it must have a reference to external function (error with op having nickname %s)\n", nick);
+		fprintf(stderr, "hip backend: op %s is registered as external but has no function to call\n", nick);
 		return -1;
 	}
 	if (f->hip_external_func(dataflow_handle, stream_id, op, f->op_extra)) {
-		fprintf(stderr, "Error: failed to do external hip function for op with nickname %s...\n", nick);
+		fprintf(stderr, "hip backend: external op %s reported an error\n", nick);
 		return -1;
 	}
 	return 0;
@@ -304,7 +307,7 @@ static int hip_submit_host_op(Dataflow_Handle * dataflow_handle, void * host_fun
 	if (resolve_stream(dataflow_handle, stream_id, &stream, "host op")) {
 		return -1;
 	}
-	HIP_CHECK_RET(hipLaunchHostFunc(stream, (hipHostFn_t) host_func, host_func_arg), -1, "failed to launch host function");
+	HIP_CHECK_RET(hipLaunchHostFunc(stream, (hipHostFn_t) host_func, host_func_arg), -1, "host function on stream");
 	return 0;
 }
 
@@ -312,12 +315,12 @@ static int hip_submit_host_op(Dataflow_Handle * dataflow_handle, void * host_fun
 
 static void * hip_get_stream_state(Dataflow_Handle * dataflow_handle, int stream_id) {
 	if (stream_id < 0 || stream_id >= dataflow_handle->num_streams) {
-		fprintf(stderr, "Error: cannot get stream state of stream id %d (device has %d streams)...\n", stream_id, dataflow_handle->num_streams);
+		fprintf(stderr, "hip backend: no stream state for stream id %d (the handle has %d streams)\n", stream_id, dataflow_handle->num_streams);
 		return NULL;
 	}
 	hipStream_t stream = ((hipStream_t *) dataflow_handle->streams)[stream_id];
 	hipEvent_t * events = (hipEvent_t *) dataflow_handle->stream_states;
-	HIP_CHECK_RET(hipEventRecord(events[stream_id], stream), NULL, "failed to record event when trying to get stream state");
+	HIP_CHECK_RET(hipEventRecord(events[stream_id], stream), NULL, "recording the stream-state event");
 	return &events[stream_id];
 }
 
@@ -327,7 +330,7 @@ static int hip_submit_dependency(Dataflow_Handle * dataflow_handle, int stream_i
 		return -1;
 	}
 	HIP_CHECK_RET(hipStreamWaitEvent(stream, *((hipEvent_t *) other_stream_state), 0), -1,
-					"failed to have current stream wait on event during submitting dependency");
+					"making the stream wait for the given state");
 	return 0;
 }
 
@@ -336,13 +339,13 @@ static int hip_sync_stream(Dataflow_Handle * dataflow_handle, int stream_id) {
 	if (resolve_stream(dataflow_handle, stream_id, &stream, "sync")) {
 		return -1;
 	}
-	HIP_CHECK_RET(hipStreamSynchronize(stream), -1, "unable to do hip stream synchronize");
+	HIP_CHECK_RET(hipStreamSynchronize(stream), -1, "synchronizing the stream");
 	return 0;
 }
 
 static int hip_sync_handle(Dataflow_Handle * dataflow_handle) {
 	HIP_CHECK_RET(hipSetDevice(dataflow_handle->device_id), -1, "device %d", dataflow_handle->device_id);
-	HIP_CHECK_RET(hipDeviceSynchronize(), -1, "was unable to sync ctx id: %d on device id: %d", dataflow_handle->ctx_id, dataflow_handle->device_id);
+	HIP_CHECK_RET(hipDeviceSynchronize(), -1, "synchronizing handle (ctx id %d) on device %d", dataflow_handle->ctx_id, dataflow_handle->device_id);
 	return 0;
 }
 
@@ -351,21 +354,21 @@ static int hip_sync_handle(Dataflow_Handle * dataflow_handle) {
 static void * hip_alloc_mem(Dataflow_Handle * dataflow_handle, uint64_t size_bytes) {
 	void * p = NULL;
 	HIP_CHECK_RET(hipSetDevice(dataflow_handle->device_id), NULL, "device %d", dataflow_handle->device_id);
-	HIP_CHECK_RET(hipMalloc(&p, (size_t) size_bytes), NULL, "failed to alloc memory on device id %d of size %lu bytes",
+	HIP_CHECK_RET(hipMalloc(&p, (size_t) size_bytes), NULL, "allocating %lu bytes on device %d",
 					dataflow_handle->device_id, (unsigned long) size_bytes);
 	return p;
 }
 
 static void hip_free_mem(Dataflow_Handle * dataflow_handle, void * dev_ptr) {
 	if (hipSetDevice(dataflow_handle->device_id) != hipSuccess || hipFree(dev_ptr) != hipSuccess) {
-		fprintf(stderr, "Error: was unable to free memory on device id %d with ptr %p...\n", dataflow_handle->device_id, dev_ptr);
+		fprintf(stderr, "hip backend: releasing device memory %p on device %d failed\n", dataflow_handle->device_id, dev_ptr);
 	}
 }
 
 static int hip_set_mem(Dataflow_Handle * dataflow_handle, int stream_id, void * dev_ptr, uint8_t val, uint64_t size_bytes) {
 	if (stream_id == -1) {
 		HIP_CHECK_RET(hipSetDevice(dataflow_handle->device_id), -1, "device %d", dataflow_handle->device_id);
-		HIP_CHECK_RET(hipMemset(dev_ptr, val, (size_t) size_bytes), -1, "was unable to set memory for device ptr of %p of %lu bytes",
+		HIP_CHECK_RET(hipMemset(dev_ptr, val, (size_t) size_bytes), -1, "filling %lu bytes at %p",
 						dev_ptr, (unsigned long) size_bytes);
 		return 0;
 	}
@@ -373,44 +376,44 @@ static int hip_set_mem(Dataflow_Handle * dataflow_handle, int stream_id, void * 
 	if (resolve_stream(dataflow_handle, stream_id, &stream, "set mem")) {
 		return -1;
 	}
-	HIP_CHECK_RET(hipMemsetAsync(dev_ptr, val, (size_t) size_bytes, stream), -1, "was unable to set memory for device ptr of %p of %lu bytes",
+	HIP_CHECK_RET(hipMemsetAsync(dev_ptr, val, (size_t) size_bytes, stream), -1, "filling %lu bytes at %p",
 					dev_ptr, (unsigned long) size_bytes);
 	return 0;
 }
 
 static int hip_enable_access_to_host_mem(Dataflow_Handle * dataflow_handle, void * host_ptr, uint64_t size_bytes, unsigned int flags) {
 	HIP_CHECK_RET(hipHostRegister(host_ptr, (size_t) size_bytes, flags), -1,
-					"failed to enable device id %d to access host memory with ptr %p of size %lu and flags %u",
+					"registering host memory %p (%lu bytes, flags %u) for device %d",
 					dataflow_handle->device_id, host_ptr, (unsigned long) size_bytes, flags);
 	return 0;
 }
 
 static int hip_disable_access_to_host_mem(Dataflow_Handle * dataflow_handle, void * host_ptr) {
-	HIP_CHECK_RET(hipHostUnregister(host_ptr), -1, "failed to disable host memory access with ptr %p from device id %d",
+	HIP_CHECK_RET(hipHostUnregister(host_ptr), -1, "unregistering host memory %p for device %d",
 					host_ptr, dataflow_handle->device_id);
 	return 0;
 }
 
 static int hip_enable_access_to_peer_mem(Dataflow_Handle * dataflow_handle, Dataflow_Handle * peer_dataflow_handle) {
 	if (peer_dataflow_handle->compute_type != dataflow_handle->compute_type) {
-		fprintf(stderr, "Error: cannot enable peer access, must be same compute type...\n");
+		fprintf(stderr, "hip backend: peer access needs two handles of the same compute type\n");
 		return -1;
 	}
 	HIP_CHECK_RET(hipSetDevice(dataflow_handle->device_id), -1, "device %d", dataflow_handle->device_id);
 	HIP_CHECK_RET(hipDeviceEnablePeerAccess(peer_dataflow_handle->device_id, 0), -1,
-					"was unable to allow this device (id %d) to access memory on peer device (id %d)",
+					"enabling access from device %d to device %d",
 					dataflow_handle->device_id, peer_dataflow_handle->device_id);
 	return 0;
 }
 
 static int hip_disable_access_to_peer_mem(Dataflow_Handle * dataflow_handle, Dataflow_Handle * peer_dataflow_handle) {
 	if (peer_dataflow_handle->compute_type != dataflow_handle->compute_type) {
-		fprintf(stderr, "Error: cannot disable peer access, must be same compute type...\n");
+		fprintf(stderr, "hip backend: peer access needs two handles of the same compute type\n");
 		return -1;
 	}
 	HIP_CHECK_RET(hipSetDevice(dataflow_handle->device_id), -1, "device %d", dataflow_handle->device_id);
 	HIP_CHECK_RET(hipDeviceDisablePeerAccess(peer_dataflow_handle->device_id), -1,
-					"was unable to disable this device (id %d) from accessing memory on peer device (id %d)",
+					"disabling access from device %d to device %d",
 					dataflow_handle->device_id, peer_dataflow_handle->device_id);
 	return 0;
 }
@@ -483,7 +486,7 @@ int init_hip_dataflow_handle(Dataflow_Handle * dataflow_handle, ComputeType comp
 								int num_streams, int * opt_stream_prios, char ** opt_stream_names) {
 	(void) ctx_flags;
 	if (num_streams < 0 || num_streams > MAX_STREAMS) {
-		fprintf(stderr, "Error: num_streams must be in [0, %d], got %d...\n", MAX_STREAMS, num_streams);
+		fprintf(stderr, "hip backend: num_streams must lie in [0, %d], got %d\n", MAX_STREAMS, num_streams);
 		return -1;
 	}
 	memset(dataflow_handle, 0, sizeof(*dataflow_handle));
@@ -492,9 +495,9 @@ int init_hip_dataflow_handle(Dataflow_Handle * dataflow_handle, ComputeType comp
 	dataflow_handle->ctx_id = ctx_id;
 
 	int count = 0;
-	HIP_CHECK_RET(hipGetDeviceCount(&count), -1, "failed to initialize the hip runtime");
+	HIP_CHECK_RET(hipGetDeviceCount(&count), -1, "counting devices");
 	if (device_id < 0 || device_id >= count) {
-		fprintf(stderr, "Error: failed to get device handle for dev id: %d (%d devices)...\n", device_id, count);
+		fprintf(stderr, "hip backend: device %d does not exist (%d devices visible)\n", device_id, count);
 		return -1;
 	}
 	HIP_CHECK_RET(hipSetDevice(device_id), -1, "device %d", device_id);
@@ -503,16 +506,16 @@ int init_hip_dataflow_handle(Dataflow_Handle * dataflow_handle, ComputeType comp
 	dataflow_handle->device_info = malloc(sizeof(Hip_Device_Info));
 	dataflow_handle->ctx = calloc(1, sizeof(Hip_Context));
 	if (!dataflow_handle->device_handle || !dataflow_handle->device_info || !dataflow_handle->ctx) {
-		fprintf(stderr, "Error: malloc failed while creating the handle...\n");
+		fprintf(stderr, "hip backend: out of host memory while creating the handle\n");
 		return init_fail(dataflow_handle);
 	}
 	*((int *) dataflow_handle->device_handle) = device_id;
 	Hip_Context * hc = (Hip_Context *) dataflow_handle->ctx;
 	hc->device_id = device_id;
 	hc->two_pass_stream = HIP_NO_STREAM;
-	HIP_CHECK_RET(hipEventCreateWithFlags(&hc->two_pass_event, hipEventDisableTiming), init_fail(dataflow_handle), "unable to create the two-pass ordering event on device id %d", device_id);
+	HIP_CHECK_RET(hipEventCreateWithFlags(&hc->two_pass_event, hipEventDisableTiming), init_fail(dataflow_handle), "creating the cross-stream ordering event on device %d", device_id);
 	if (hip_set_device_info((Hip_Device_Info *) dataflow_handle->device_info, device_id)) {
-		fprintf(stderr, "Error: was unable to set hip device info for dev id: %d...\n", device_id);
+		fprintf(stderr, "hip backend: reading the properties of device %d failed\n", device_id);
 		return init_fail(dataflow_handle);
 	}
 
@@ -521,14 +524,14 @@ int init_hip_dataflow_handle(Dataflow_Handle * dataflow_handle, ComputeType comp
 	for (int i = 0; i < MAX_STREAMS; i++) {
 		dataflow_handle->stream_prios[i] = (i < num_streams) ? (opt_stream_prios ? opt_stream_prios[i] : HIP_DEFAULT_STREAM_PRIO) : -1;
 		if (i < num_streams && dataflow_handle->stream_prios[i] != HIP_DEFAULT_STREAM_PRIO && !warned) {
-			fprintf(stderr, "Warning: stream priorities are recorded but every stream is created at the default priority...\n");
+			fprintf(stderr, "hip backend: warning: stream priorities are recorded, but every stream runs at the default priority\n");
 			warned = true;
 		}
 		dataflow_handle->stream_names[i] = NULL;
 		if (i < num_streams && opt_stream_names && opt_stream_names[i]) {
 			dataflow_handle->stream_names[i] = strdup(opt_stream_names[i]);
 			if (!dataflow_handle->stream_names[i]) {
-				fprintf(stderr, "Error: failed to alloc space to hold stream name...\n");
+				fprintf(stderr, "hip backend: out of host memory for a stream name\n");
 				return init_fail(dataflow_handle);
 			}
 		}
@@ -538,21 +541,21 @@ int init_hip_dataflow_handle(Dataflow_Handle * dataflow_handle, ComputeType comp
 	dataflow_handle->streams = calloc(ns, sizeof(hipStream_t));
 	dataflow_handle->stream_states = calloc(ns, sizeof(hipEvent_t));
 	if (!dataflow_handle->streams || !dataflow_handle->stream_states) {
-		fprintf(stderr, "Error: malloc failed to allocate stream containers...\n");
+		fprintf(stderr, "hip backend: out of host memory for the stream tables\n");
 		return init_fail(dataflow_handle);
 	}
 	hipStream_t * streams = (hipStream_t *) dataflow_handle->streams;
 	hipEvent_t * events = (hipEvent_t *) dataflow_handle->stream_states;
 	for (int i = 0; i < num_streams; i++) {
-		HIP_CHECK_RET(hipStreamCreateWithFlags(&streams[i], hipStreamNonBlocking), init_fail(dataflow_handle), "unable to initialize stream #%d on device id %d", i, device_id);
-		HIP_CHECK_RET(hipEventCreateWithFlags(&events[i], hipEventDisableTiming), init_fail(dataflow_handle), "unable to initialize event for stream #%d on device id %d", i, device_id);
+		HIP_CHECK_RET(hipStreamCreateWithFlags(&streams[i], hipStreamNonBlocking), init_fail(dataflow_handle), "creating stream %d on device %d", i, device_id);
+		HIP_CHECK_RET(hipEventCreateWithFlags(&events[i], hipEventDisableTiming), init_fail(dataflow_handle), "creating the state event of stream %d on device %d", i, device_id);
 	}
 
 	dataflow_handle->num_native_function_libs = 0;
 	dataflow_handle->num_ops = 0;
 	if (init_table(&dataflow_handle->op_table, hip_op_table_hash_func, OP_IDENTIFIER_FINGERPRINT_NUM_BYTES, sizeof(Hip_Function),
 					OP_TABLE_MIN_SIZE, OP_TABLE_MAX_SIZE, 1.0f, 1.0f)) {
-		fprintf(stderr, "Error: failed to init op table...\n");
+		fprintf(stderr, "hip backend: the op table could not be created\n");
 		return init_fail(dataflow_handle);
 	}
 

@@ -41,6 +41,11 @@ int rms_norm_set_attribute_config(Dataflow_Handle * dataflow_handle, Hip_Functio
 		return -1;
 	}
 	hip_function->function_config.func_max_threads_per_block = max_threads;
+	/* the dW ops (bwd_w and the fused bwd, not bwd_x) reduce through the
+	 * module's partial-row scratch */
+	const char * nick = hip_function->op_skeleton.header.op_nickname;
+	hip_function->function_config.shares_module_scratch =
+		strncmp(nick, "rms_norm_bwd_", 13) == 0 && strncmp(nick, "rms_norm_bwd_x_", 15) != 0;
 	return 0;
 }
 
@@ -52,10 +57,20 @@ static int rms_check(const char * what, int n_rows, int n_cols, size_t elem) {
 	return 0;
 }
 
-/* workgroups of this function that are resident on the whole device at once */
+/* workgroups of this function that are resident on the whole device at once;
+ * the occupancy query is remembered per function for the last (block, LDS)
+ * pair asked, so repeated submits of one shape do not repeat it */
 static long resident_groups(Dataflow_Handle * h, Hip_Function * f, int block, size_t lds) {
+	const uint64_t key = ((uint64_t) (unsigned) block << 40) | ((uint64_t) (lds & 0xffffffull) << 16);
+	const uint64_t memo = __atomic_load_n(&f->function_config.occupancy_memo, __ATOMIC_RELAXED);
 	int per_cu = 0;
-	if (hipModuleOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, f->function_handle, block, lds) != hipSuccess || per_cu < 1) per_cu = 1;
+	if (memo != 0 && (memo & ~0xffffull) == key) {
+		per_cu = (int) (memo & 0xffffull);
+	}
+	else {
+		if (hipModuleOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, f->function_handle, block, lds) != hipSuccess || per_cu < 1) per_cu = 1;
+		if (lds <= 0xffffffull && per_cu <= 0xffff) __atomic_store_n(&f->function_config.occupancy_memo, key | (uint64_t) per_cu, __ATOMIC_RELAXED);
+	}
 	return (long) per_cu * (long) dev(h)->cu_count;
 }
 

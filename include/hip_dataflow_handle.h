@@ -50,6 +50,14 @@ typedef struct hip_device_info {
 typedef struct hip_function_config {
 	int func_max_smem;
 	int func_max_threads_per_block;
+	/* set by the launch-config library's init for functions whose kernels keep
+	 * per-launch partial results in the code object's module-scope scratch:
+	 * the handle orders such functions across its streams (Hip_Context) */
+	int shares_module_scratch;
+	/* last occupancy query of the launch-config library, packed as
+	 * block << 40 | LDS bytes << 16 | workgroups per CU (0: none yet); read and
+	 * written as one 64-bit word, so concurrent submits see a whole entry */
+	uint64_t occupancy_memo;
 } Hip_Function_Config;
 
 typedef struct hip_launch_config {
@@ -91,16 +99,17 @@ typedef int (*Hip_Set_Func_Attribute)(Dataflow_Handle * dataflow_handle, Hip_Fun
 
 /* What Dataflow_Handle.ctx points to (HIP has no per-handle contexts; the
  * CUDA backend keeps its CUcontext there). The device id comes first, so ctx
- * still reads as the device id. Two-pass ops (native ops with a finish
- * kernel) keep per-launch partial results in their code object's
- * module-scope scratch, so the handle orders them across its streams: a
- * two-pass op submitted on another stream than the previous one first waits
- * for everything then queued on that stream (an event recorded only when the
- * stream changes, so single-stream use pays nothing). */
+ * still reads as the device id. Functions flagged shares_module_scratch (the
+ * RMSNorm dW ops) keep per-launch partial results in their code object's
+ * module-scope scratch, so the handle orders them across its streams: such
+ * an op submitted on another stream than the previous one first waits for
+ * everything then queued on that stream (an event recorded only when the
+ * stream changes, so single-stream use pays nothing). Other ops, the fused
+ * cross-entropy's two kernels included, are not ordered. */
 #define HIP_NO_STREAM INT_MIN
 typedef struct hip_context {
 	int device_id;
-	int two_pass_stream;       /* stream id of the last two-pass op, HIP_NO_STREAM before the first */
+	int two_pass_stream;       /* stream id of the last scratch-sharing op, HIP_NO_STREAM before the first */
 	hipEvent_t two_pass_event;
 } Hip_Context;
 
