@@ -21,6 +21,8 @@ CORE_LIB = os.path.join(LIB_DIR, "libdataflow.so")
 CONFIG_LIB = os.path.join(LIB_DIR, "libdataflow_hip_config.so")
 KERNELS = os.path.join(LIB_DIR, "dataflow_kernels_gfx950.hsaco")
 MATMUL_LIB = os.path.join(LIB_DIR, "libdataflow_hipblaslt.so")
+# measurement only: streaming copies bench.py times as the memory ceiling
+BENCH_COPY_KERNELS = os.path.join(LIB_DIR, "bench_stream_copy_gfx950.hsaco")
 
 # ---- enums (values are part of op fingerprints; never reorder) ----
 DATAFLOW_NONE, DATAFLOW_VOID, DATAFLOW_FP64, DATAFLOW_FP32, DATAFLOW_FP16, DATAFLOW_BF16 = range(6)

@@ -6,6 +6,8 @@ Outputs (in-tree, under dataflow_lib_amd/lib/):
   libdataflow_hip_config.so      launch configurations (dlopen'ed by the backend)
   dataflow_kernels_gfx950.hsaco  gfx950 code object (hipModuleLoad'ed by the backend)
   libdataflow_hipblaslt.so       the external matmul op on hipBLASLt (register_external_matmul)
+  bench_stream_copy_gfx950.hsaco streaming copies bench.py times as the memory system's
+                                 ceiling (not part of the product; loaded by bench.py only)
 """
 import os
 import shutil
@@ -26,6 +28,7 @@ KERNELS_OUT = os.path.join(LIB, "dataflow_kernels_gfx950.hsaco")
 CORE_OUT = os.path.join(LIB, "libdataflow.so")
 CONFIG_OUT = os.path.join(LIB, "libdataflow_hip_config.so")
 MATMUL_OUT = os.path.join(LIB, "libdataflow_hipblaslt.so")
+BENCH_COPY_OUT = os.path.join(LIB, "bench_stream_copy_gfx950.hsaco")
 CXX = os.environ.get("CXX", "g++")
 
 C_FLAGS = ["-O2", "-fPIC", "-std=gnu11", "-Wall", "-Wextra", "-Wno-unused-parameter", "-Wno-stringop-truncation",
@@ -81,7 +84,8 @@ def build(verbose=False):
                                         "-I", INCLUDE, "-I", os.path.join(ROCM, "include"),
                                         os.path.join(CSRC, "external", "hipblaslt_matmul.cpp"), "-o", o,
                                         "-L", os.path.join(ROCM, "lib"), "-lhipblaslt"] + HIP_LINK, verbose))
-    return {"kernels": KERNELS_OUT, "core": CORE_OUT, "config": CONFIG_OUT, "matmul": MATMUL_OUT}
+    _atomic(BENCH_COPY_OUT, lambda o: _run([HIPCC] + HIP_FLAGS + [os.path.join(CSRC, "bench", "stream_copy.hip"), "-o", o], verbose))
+    return {"kernels": KERNELS_OUT, "core": CORE_OUT, "config": CONFIG_OUT, "matmul": MATMUL_OUT, "bench_copy": BENCH_COPY_OUT}
 
 
 if __name__ == "__main__":

@@ -1,6 +1,8 @@
 /*
  * Streaming copies used only as a measurement reference (bench.py's
- * copy_reference; no op skeleton is registered for them): dst = src over
+ * copy_reference). Built into a code object of their own
+ * (lib/bench_stream_copy_gfx950.hsaco) that bench.py loads itself; the
+ * product code object does not contain them. dst = src over
  * nchunks 16-byte chunks with non-temporal 16-byte buffer accesses, all of a
  * step's loads issued before its stores - the access patterns of the path's
  * kernels without their arithmetic. Two orders:

@@ -8,4 +8,3 @@
 #include "swiglu.hip"
 #include "softmax_xent.hip"
 #include "gather_scatter.hip"
-#include "stream_copy.hip"

@@ -62,3 +62,7 @@ def test_kernel_code_object_present():
                 b"swiglu_bwd_x_bf16_bf16_kernel", b"softmax_cross_entropy_loss_bf16_kernel", b"embedding_fp8e5m2_kernel",
                 b"copy_to_seq_context_bf16_kernel", b"rope_copy_to_seq_context_bf16_kernel"):
         assert sym in data
+    # the measurement-only streaming copies live in bench.py's own code object
+    assert b"dataflow_stream_copy" not in data
+    bench = open(api.BENCH_COPY_KERNELS, "rb").read()
+    assert b"dataflow_stream_copy_blk8_kernel" in bench
