@@ -15,13 +15,14 @@ Inputs are resident in HBM before timing. Each op rotates through enough
 buffer sets that its working set per rotation is >= 1 GiB, so the 256 MB
 Infinity Cache cannot serve repeats. The K timed steps run back to back
 between two events on the launch stream (an event between kernels would add
-several microseconds of stream time to every op). K defaults to 100: the
-timed region starts after a synchronize, and the first launches into the idle
-GPU cost about 0.5 ms once, which at K = 20 added ~25 us to every step (847
-against 821 us of per-op time) and at K = 100 ~8 us; `value` = sum of per-op
-algorithmic bytes / measured step time. Per-op time = the average launch
-duration of K back-to-back launches of that op alone (rotating its sets),
-between two events on the launch stream. Timed as extras, outside `value`: the
+several microseconds of stream time to every op). The start event is recorded
+behind the queued warm-up launches, with no host synchronization in between,
+so the GPU is busy when it fires: the timed region is steady state at any K
+(a start from an idle GPU once cost about 0.5 ms, ~25 us per step at K = 20).
+`value` = sum of per-op algorithmic bytes / measured step time. Per-op time =
+the average launch duration of K back-to-back launches of that op alone
+(rotating its sets, behind a few queued untimed launches), between two events
+on the launch stream. Timed as extras, outside `value`: the
 reference-compatible split ops (rms_norm_bwd_x, rms_norm_bwd_w, softmax,
 cross_entropy_loss) and the path's neighbours (embedding gather of 8192 rows
 of a 128256 x 4096 bf16 table; copy_to_seq_context of K, V [8192 x 1024] bf16
@@ -31,7 +32,8 @@ the loss-path driver
 (submit_transformer_head, training pass) at 4096 tokens x 4096 x 128256, whose
 time is its three hipBLASLt GEMMs (reported in TFLOP/s).
 
-copy_reference: per op, the code object's streaming copy moving the same
+copy_reference: per op, a streaming copy (a code object of its own, not the
+product's) moving the same
 total bytes (half read, half written), timed the same way - the ceiling the
 memory system offers that many bytes (the op's time over it is reported).
 
@@ -297,19 +299,30 @@ def build_extras(h, pool, api):
     return ops
 
 
+# launches queued ahead of every timed batch of one op (and of every copy
+# shape), so that its start event fires while the GPU is busy
+PREROLL = 3
+
+
 def time_ops(h, hip, ops, steps, warmup, batches=5):
     """Time `steps` steps (each op once per step, rotating buffer sets) on one
     stream, with events only at the two ends (an event recorded between
     kernels costs the stream several microseconds, which would be counted as
-    the ops' time). Then, for the per-op figures, each op alone: `steps`
-    launches back to back over its rotating sets, again timed from two events,
-    in `batches` batches; the op's time is the median batch's average launch
-    duration (kernel plus the gap to the next launch)."""
+    the ops' time). The host synchronizes before the `warmup` steps and after
+    the timed ones; the start event is recorded right behind the queued
+    warm-up launches, with no synchronization in between, so it fires when the
+    warm-up's last kernel ends and the timed region is steady state whatever
+    `steps` is (a start event recorded on an idle GPU charges the ramp from
+    idle to the first timed steps). Then, for the per-op figures, each op
+    alone: `steps` launches back to back over its rotating sets, again timed
+    from two events and again behind PREROLL queued launches, in `batches`
+    batches; the op's time is the median batch's average launch duration
+    (kernel plus the gap to the next launch)."""
     stream = h.stream(0)
+    h.sync()
     for w in range(warmup):
         for name, _, runs in ops:
             assert runs[w % len(runs)]() == 0, name
-    h.sync()
     a, b = hip.event(), hip.event()
     t0 = time.perf_counter()
     hip.record(a, stream)
@@ -324,6 +337,8 @@ def time_ops(h, hip, ops, steps, warmup, batches=5):
     for name, nbytes, runs in ops:
         avgs = []
         for _ in range(batches):
+            for k in range(PREROLL):
+                assert runs[(steps + k) % len(runs)]() == 0, name
             hip.record(a, stream)
             for k in range(steps):
                 assert runs[k % len(runs)]() == 0, name
@@ -340,8 +355,8 @@ def time_ops(h, hip, ops, steps, warmup, batches=5):
 
 
 def copy_reference(h, hip, pool, api, per_op, launches):
-    """What the memory system offers each op's byte count: the code object's
-    streaming copy (dataflow_stream_copy_*: non-temporal 16-byte buffer loads
+    """What the memory system offers each op's byte count: the bench code
+    object's streaming copy (dataflow_stream_copy_*: non-temporal 16-byte buffer loads
     then stores, grid-stride) moving the same total bytes half read, half
     written, timed like the ops (back-to-back launches over at least two
     rotating buffer sets, >= 2 GiB per rotation, between two events; median of three
@@ -355,7 +370,7 @@ def copy_reference(h, hip, pool, api, per_op, launches):
     shapes = [("dataflow_stream_copy_u2_kernel", m * cu, 512) for m in (2, 3, 4)] + [
         ("dataflow_stream_copy_u4_kernel", cu, 1024), ("dataflow_stream_copy_blk8_kernel", cu, 1024),
         ("dataflow_stream_copy_blk16_kernel", 2 * cu, 512)]
-    fns = [(hip.module_function(api.KERNELS, n), g, b) for n, g, b in shapes]
+    fns = [(hip.module_function(api.BENCH_COPY_KERNELS, n), g, b) for n, g, b in shapes]
     out = {}
     a, b = hip.event(), hip.event()
     for name, op in per_op.items():
@@ -366,10 +381,10 @@ def copy_reference(h, hip, pool, api, per_op, launches):
         for (f, grid, block), (kname, _, _) in zip(fns, shapes):
             run = lambda i: hip.launch(f, grid, block, [ctypes.c_void_p(bufs[i % sets][0]), ctypes.c_void_p(bufs[i % sets][1]),
                                                          ctypes.c_uint64(half // 16)], stream)
-            for i in range(3):
-                run(i)
             batch = []
             for _ in range(3):
+                for i in range(PREROLL):
+                    run(launches + i)
                 hip.record(a, stream)
                 for i in range(launches):
                     run(i)
