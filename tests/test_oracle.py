@@ -223,6 +223,53 @@ def test_rope_bruteforce_rotation_matrix_and_inverse():
     assert np.allclose(back, Q, rtol=1e-6, atol=1e-6)
 
 
+def textbook_rope(X, pos, hd, theta, inverse=False):
+    """RoFormer rotation in fp64 of every head of X [T x heads*hd]: pair
+    (2p, 2p+1) turns by pos * theta^(-2p/hd), with the angle, the position and
+    their product rounded to fp32 the way the reference forms them
+    (attention/rope.cu:26-33) and cos/sin rounded to fp32; written from the
+    formula, independently of the oracle's indexing."""
+    T, width = X.shape
+    out = np.empty((T, width), np.float64)
+    for t in range(T):
+        for j in range(0, width, 2):
+            p = (j % hd) // 2
+            ang = np.float32(np.power(np.float64(theta), np.float64(np.float32(-(np.float32(2 * p) / np.float32(hd))))))
+            arg = np.float32(np.float32(pos[t]) * ang)
+            c, s = np.float64(np.float32(np.cos(np.float64(arg)))), np.float64(np.float32(np.sin(np.float64(arg))))
+            if inverse:
+                s = -s
+            e, o = np.float64(X[t, j]), np.float64(X[t, j + 1])
+            out[t, j], out[t, j + 1] = c * e - s * o, c * o + s * e
+    return out
+
+
+def test_rope_k_rows_against_textbook_rotation():
+    """The K path on its own row width: fewer K heads than Q heads (kv_dim !=
+    model_dim), several tokens and positions other than 0, so a K row
+    addressed with Q's row width, or a K head given Q's table, fails."""
+    hd, nq, nkv, theta = 16, 4, 2, 500000
+    pos = np.array([0, 1, 5, 77, 2047, 123456], np.int32)
+    T = pos.size
+    Q, K = normal(24, (T, nq * hd)), normal(25, (T, nkv * hd))
+    for bwd in (0, 1):
+        qv, kv = rope(FP32, bwd, Q, K, pos, hd, nkv, theta)
+        assert np.allclose(qv, textbook_rope(Q, pos, hd, theta, inverse=bool(bwd)), rtol=1e-14, atol=1e-14)
+        assert np.allclose(kv, textbook_rope(K, pos, hd, theta, inverse=bool(bwd)), rtol=1e-14, atol=1e-14)
+        # every K pair keeps its length
+        n0 = (K.astype(np.float64).reshape(T, -1, 2) ** 2).sum(-1)
+        assert np.allclose((kv.reshape(T, -1, 2) ** 2).sum(-1), n0, rtol=1e-6)
+    # bwd(fwd(K)) = K up to the fp32 storage of fwd(K), on K rows alone
+    _, kv = rope(FP32, 0, Q, K, pos, hd, nkv, theta)
+    _, back = rope(FP32, 1, Q, kv.astype(np.float32), pos, hd, nkv, theta)
+    assert np.allclose(back, K, rtol=1e-6, atol=1e-6)
+    # bf16 K: the oracle's pre-rounding values are the fp64 rotation of the
+    # bf16 inputs
+    Kb = to_storage(K, BF16)
+    _, kvb = rope(BF16, 0, to_storage(Q, BF16), Kb, pos, hd, nkv, theta)
+    assert np.allclose(kvb, textbook_rope(to_f64(Kb, BF16), pos, hd, theta), rtol=1e-14, atol=1e-14)
+
+
 # ---------------- SwiGLU ----------------
 
 def sw(dt, g, u, dO):
