@@ -21,6 +21,7 @@ CORE_LIB = os.path.join(LIB_DIR, "libdataflow.so")
 CONFIG_LIB = os.path.join(LIB_DIR, "libdataflow_hip_config.so")
 KERNELS = os.path.join(LIB_DIR, "dataflow_kernels_gfx950.hsaco")
 MATMUL_LIB = os.path.join(LIB_DIR, "libdataflow_hipblaslt.so")
+NOALLOC_LIB = os.path.join(LIB_DIR, "libdataflow_noalloc.so")
 # measurement only: streaming copies bench.py times as the memory ceiling
 BENCH_COPY_KERNELS = os.path.join(LIB_DIR, "bench_stream_copy_gfx950.hsaco")
 
@@ -169,6 +170,31 @@ def _declare(L):
     L.submit_softmax.argtypes = [h, s, i, i, i, i, vp, vp]
     L.submit_cross_entropy_loss.argtypes = [h, s, i, i, i, vp, vp]
     L.submit_softmax_cross_entropy_loss.argtypes = [h, s, i, i, i, vp, vp, vp, vp]
+
+
+_noalloc = None
+
+
+def noalloc_lib():
+    """The loaded libdataflow_noalloc.so (raises when it has not been built)."""
+    global _noalloc
+    if _noalloc is None:
+        if not os.path.exists(NOALLOC_LIB):
+            raise RuntimeError("native library %s is missing: run __graft_entry__.build() first" % NOALLOC_LIB)
+        lib()   # its dependency, loaded from the same directory
+        L = ctypes.CDLL(NOALLOC_LIB)
+        i, f32, vp = ctypes.c_int, ctypes.c_float, ctypes.c_void_p
+        L.dataflow_rms_norm_bwd_noalloc.argtypes = [vp, i, i, i, i, f32, vp, vp, vp, vp, vp, vp]
+        L.dataflow_rms_norm_bwd_noalloc.restype = i
+        _noalloc = L
+    return _noalloc
+
+
+def rms_norm_bwd_noalloc(stream, fwd_dt, bwd_dt, n_rows, n_cols, eps, fwd_rms_vals, rms_weight, X_inp, upstream_dX, dX, dW):
+    """dataflow_rms_norm_bwd_noalloc (include/dataflow_noalloc.h): submit_rms_norm_bwd's
+    computation on a hipStream_t, with no handle and no allocation."""
+    return noalloc_lib().dataflow_rms_norm_bwd_noalloc(stream, fwd_dt, bwd_dt, n_rows, n_cols, eps, fwd_rms_vals,
+                                                       rms_weight, X_inp, upstream_dX, dX, dW)
 
 
 def datatype_as_string(dt):

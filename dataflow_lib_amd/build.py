@@ -6,6 +6,8 @@ Outputs (in-tree, under dataflow_lib_amd/lib/):
   libdataflow_hip_config.so      launch configurations (dlopen'ed by the backend)
   dataflow_kernels_gfx950.hsaco  gfx950 code object (hipModuleLoad'ed by the backend)
   libdataflow_hipblaslt.so       the external matmul op on hipBLASLt (register_external_matmul)
+  libdataflow_noalloc.so         the allocation-free entry point (include/dataflow_noalloc.h):
+                                 host code and its gfx950 kernels in one HIP fat binary
   bench_stream_copy_gfx950.hsaco streaming copies bench.py times as the memory system's
                                  ceiling (not part of the product; loaded by bench.py only)
 """
@@ -29,6 +31,7 @@ CORE_OUT = os.path.join(LIB, "libdataflow.so")
 CONFIG_OUT = os.path.join(LIB, "libdataflow_hip_config.so")
 MATMUL_OUT = os.path.join(LIB, "libdataflow_hipblaslt.so")
 BENCH_COPY_OUT = os.path.join(LIB, "bench_stream_copy_gfx950.hsaco")
+NOALLOC_OUT = os.path.join(LIB, "libdataflow_noalloc.so")
 CXX = os.environ.get("CXX", "g++")
 
 C_FLAGS = ["-O2", "-fPIC", "-std=gnu11", "-Wall", "-Wextra", "-Wno-unused-parameter", "-Wno-stringop-truncation",
@@ -84,8 +87,14 @@ def build(verbose=False):
                                         "-I", INCLUDE, "-I", os.path.join(ROCM, "include"),
                                         os.path.join(CSRC, "external", "hipblaslt_matmul.cpp"), "-o", o,
                                         "-L", os.path.join(ROCM, "lib"), "-lhipblaslt"] + HIP_LINK, verbose))
+    _atomic(NOALLOC_OUT, lambda o: _run([HIPCC, "--offload-arch=" + ARCH, "-O3", "-std=c++17", "-fPIC", "-shared",
+                                         "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+                                         "-I", INCLUDE, "-I", os.path.join(CSRC, "kernels"),
+                                         os.path.join(CSRC, "noalloc", "rms_norm_bwd_noalloc.hip"), "-o", o,
+                                         "-L", LIB, "-ldataflow", "-Wl,-rpath,$ORIGIN"], verbose))
     _atomic(BENCH_COPY_OUT, lambda o: _run([HIPCC] + HIP_FLAGS + [os.path.join(CSRC, "bench", "stream_copy.hip"), "-o", o], verbose))
-    return {"kernels": KERNELS_OUT, "core": CORE_OUT, "config": CONFIG_OUT, "matmul": MATMUL_OUT, "bench_copy": BENCH_COPY_OUT}
+    return {"kernels": KERNELS_OUT, "core": CORE_OUT, "config": CONFIG_OUT, "matmul": MATMUL_OUT,
+            "noalloc": NOALLOC_OUT, "bench_copy": BENCH_COPY_OUT}
 
 
 if __name__ == "__main__":

@@ -74,16 +74,6 @@ static long resident_groups(Dataflow_Handle * h, Hip_Function * f, int block, si
 	return (long) per_cu * (long) dev(h)->cu_count;
 }
 
-/* Row slots per CU for the row-streaming RMSNorm ops: each slot keeps two rows
- * of `arrays` input rows in flight (the current one and the prefetched next
- * one), and about RMS_INFLIGHT_BYTES outstanding per CU measured best: more
- * concurrent row streams only add DRAM page misses. */
-static long rms_slots_per_cu(int n_cols, size_t elem, int arrays) {
-	const long per_slot = 2L * (long) n_cols * (long) elem * (long) arrays;
-	long s = per_slot > 0 ? (long) RMS_INFLIGHT_BYTES / per_slot : 1;
-	return MY_MAX(1L, MY_MIN(s, 32L));
-}
-
 /* fwd / bwd_x: ~256-thread workgroups, as many per CU as the slot target asks */
 static void rms_rowwise(Hip_Launch_Config * c, Dataflow_Handle * h, Hip_Function * f, int n_rows, int n_cols, size_t elem, int nv, int arrays) {
 	const int tpr = rms_tpr_for(nv);
@@ -92,7 +82,7 @@ static void rms_rowwise(Hip_Launch_Config * c, Dataflow_Handle * h, Hip_Function
 	const unsigned lds = (unsigned) (RMS_CELLS_PER_SLOT * slots * sizeof(float));
 	/* the element path (nv == 0) walks its rows with plain loads and keeps no
 	 * row in flight ahead, so it needs many rows per CU to hide latency */
-	const long groups_per_cu = (nv == 0) ? RMS_STREAM_GROUPS_PER_CU : MY_CEIL(rms_slots_per_cu(n_cols, elem, arrays), (long) slots);
+	const long groups_per_cu = (nv == 0) ? RMS_STREAM_GROUPS_PER_CU : MY_CEIL(rms_slots_per_cu(n_cols, (long) elem, arrays), (long) slots);
 	long grid = MY_MIN((long) MY_CEIL(n_rows, slots), (long) dev(h)->cu_count * groups_per_cu);
 	grid = MY_MIN(grid, resident_groups(h, f, (int) block, lds));
 	set_1d(c, (unsigned) grid, block, lds);
@@ -117,35 +107,26 @@ int rms_norm_bwd_x_set_launch_config(Hip_Launch_Config * hip_launch_config, Data
 	return 0;
 }
 
-/* two-pass dW ops: pick slots and grid so LDS and the partial scratch fit */
+/* two-pass dW ops: slots and grid so LDS and the partial scratch fit
+ * (rms_dw_geometry, shared with the allocation-free entry point) */
 static int rms_dw_config(Hip_Launch_Config * c, Dataflow_Handle * h, Hip_Function * f, const char * what, int n_rows, int n_cols, size_t elem, int nv, int arrays) {
 	if (n_rows == 0 || n_cols == 0) {
 		set_1d(c, 0, 1, 0);
 		return 0;
 	}
-	const int tpr = (nv > 0) ? rms_tpr_for(nv) : rms_stream_tpr(1, n_cols);
 	const long max_lds = f->function_config.func_max_smem > 0 ? f->function_config.func_max_smem : dev(h)->max_smem_per_block;
-	/* one workgroup per CU holding the CU's row slots (one dW partial row per
-	 * workgroup) */
-	int slots = (int) MY_MIN(rms_slots_per_cu(n_cols, elem, arrays), (long) MY_MAX(1, RMS_MAX_TPR / tpr));
-	long lds = 0;
-	for (; slots >= 1; slots--) {
-		const long colbuf = (nv > 0) ? (long) n_cols : (long) slots * n_cols;
-		lds = (long) (RMS_CELLS_PER_SLOT * slots + colbuf) * (long) sizeof(float);
-		if (lds <= max_lds) break;
-	}
-	if (slots < 1) {
+	unsigned grid = 0, block = 0, lds = 0;
+	const int rc = rms_dw_geometry(n_rows, n_cols, (long) elem, nv, arrays, (long) dev(h)->cu_count, max_lds,
+								   (long) RMS_DW_SCRATCH_FLOATS, &grid, &block, &lds);
+	if (rc == -1) {
 		fprintf(stderr, "Error: %s: rows of %d columns need more LDS than the %ld bytes available...\n", what, n_cols, max_lds);
 		return -1;
 	}
-	const long max_parts = (long) RMS_DW_SCRATCH_FLOATS / (long) n_cols;
-	if (max_parts < 1) {
+	if (rc != 0) {
 		fprintf(stderr, "Error: %s: %d columns exceed the dW scratch of %u floats...\n", what, n_cols, (unsigned) RMS_DW_SCRATCH_FLOATS);
 		return -1;
 	}
-	long grid = MY_MIN((long) MY_CEIL((long) n_rows, (long) slots), (long) dev(h)->cu_count);
-	grid = MY_MIN(grid, max_parts);
-	set_1d(c, (unsigned) grid, (unsigned) (slots * tpr), (unsigned) lds);
+	set_1d(c, grid, block, lds);
 	return 0;
 }
 

@@ -96,6 +96,47 @@ GEOM_FN int rms_tpr_for(int nv) {
 	return ((t + 63) / 64) * 64;
 }
 
+/* Row slots per CU for the row-streaming RMSNorm ops: each slot keeps two rows
+ * of `arrays` input rows in flight (the current one and the prefetched next
+ * one), and about RMS_INFLIGHT_BYTES outstanding per CU measured best: more
+ * concurrent row streams only add DRAM page misses. */
+GEOM_FN long rms_slots_per_cu(int n_cols, long elem, int arrays) {
+	const long per_slot = 2L * (long) n_cols * elem * (long) arrays;
+	const long s = per_slot > 0 ? (long) RMS_INFLIGHT_BYTES / per_slot : 1;
+	return s < 1 ? 1 : (s > 32 ? 32 : s);
+}
+
+/* Launch shape of the dW ops (bwd_w: arrays = 2, fused bwd: arrays = 3) for
+ * n_rows >= 1 and n_cols >= 1: one workgroup per CU holding the CU's row
+ * slots, so each workgroup writes one fp32 partial row. nv is
+ * rms_vec_chunks(); max_lds the LDS bytes a workgroup may use; scratch_floats
+ * the size of the partial-row buffer. Fills grid, block and dynamic LDS bytes
+ * and returns 0, or -1 when the LDS cannot hold a row's partial sums, -2 when
+ * one partial row does not fit the buffer. */
+GEOM_FN int rms_dw_geometry(int n_rows, int n_cols, long elem, int nv, int arrays, long cu_count, long max_lds,
+							long scratch_floats, unsigned * grid, unsigned * block, unsigned * lds) {
+	const int tpr = (nv > 0) ? rms_tpr_for(nv) : rms_stream_tpr(1, n_cols);
+	const long by_slots = rms_slots_per_cu(n_cols, elem, arrays);
+	const long by_threads = (RMS_MAX_TPR / tpr) < 1 ? 1 : (RMS_MAX_TPR / tpr);
+	int slots = (int) (by_slots < by_threads ? by_slots : by_threads);
+	long bytes = 0;
+	for (; slots >= 1; slots--) {
+		const long colbuf = (nv > 0) ? (long) n_cols : (long) slots * n_cols;
+		bytes = ((long) RMS_CELLS_PER_SLOT * slots + colbuf) * (long) sizeof(float);
+		if (bytes <= max_lds) break;
+	}
+	if (slots < 1) return -1;
+	const long max_parts = scratch_floats / (long) n_cols;
+	if (max_parts < 1) return -2;
+	long g = ((long) n_rows + slots - 1) / slots;
+	if (g > cu_count) g = cu_count;
+	if (g > max_parts) g = max_parts;
+	*grid = (unsigned) g;
+	*block = (unsigned) (slots * tpr);
+	*lds = (unsigned) bytes;
+	return 0;
+}
+
 /* RoPE: whether the vector (slot) path applies */
 GEOM_FN int rope_slot_ok(int model_dim, int kv_dim, int head_dim, int elem_bytes, unsigned long long ptr_or) {
 	const int vec = 16 / elem_bytes;

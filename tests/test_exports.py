@@ -37,11 +37,12 @@ def declared_functions(path):
 def test_every_declared_symbol_is_exported():
     core = api.lib()
     cfg = ctypes.CDLL(api.CONFIG_LIB)
+    noalloc = api.noalloc_lib()
     headers = sorted(f for f in os.listdir(INCLUDE) if f.endswith(".h"))
     seen = 0
     for h in headers:
         names = declared_functions(os.path.join(INCLUDE, h))
-        lib = cfg if h == "hip_ops_config.h" else core
+        lib = {"hip_ops_config.h": cfg, "dataflow_noalloc.h": noalloc}.get(h, core)
         missing = [n for n in names if not hasattr(lib, n)]
         assert not missing, "%s declares functions missing from %s: %s" % (h, lib._name, missing)
         seen += len(names)
