@@ -166,15 +166,24 @@ __device__ __forceinline__ void rms_vector(const RmsArgs & a, int nv, float * ld
 		const __amdgpu_buffer_rsrc_t ro = row_rsrc(a.Y_or_dX, row, a.n_rows, row_bytes);
 
 		if (MODE == RMS_FWD) {
-			float ss = 0.0f, sw = 0.0f;
+			/* four interleaved partial sums (chunk, element parity) per thread,
+			 * added pairwise: the fp32 rounding chain of a term is 4 + 2 long
+			 * instead of RMS_CH * V */
+			float ssp[4] = {0.0f, 0.0f, 0.0f, 0.0f}, swp[4] = {0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
 			for (int c = 0; c < RMS_CH; c++) {
 				float xf[V], wf[V];
 				unpack16<T>(cur.x[c], xf);
 				unpack16<T>(wr[c], wf);
 #pragma unroll
-				for (int e = 0; e < V; e++) { sw = fmaf(xf[e], wf[e], sw); ss = fmaf(xf[e], xf[e], ss); }
+				for (int e = 0; e < V; e++) {
+					const int k = (c * 2 + (e & 1)) & 3;
+					swp[k] = fmaf(xf[e], wf[e], swp[k]);
+					ssp[k] = fmaf(xf[e], xf[e], ssp[k]);
+				}
 			}
+			float ss = (ssp[0] + ssp[1]) + (ssp[2] + ssp[3]);
+			float sw = (swp[0] + swp[1]) + (swp[2] + swp[3]);
 			slot_sum2(ss, sw, cells, parity, slot, wis, wps, slots);
 			parity ^= 1;
 #pragma unroll

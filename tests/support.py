@@ -144,3 +144,82 @@ def check_f32(o, v, rel=1e-5, floor=None, what=""):
         k = bad[0]
         raise AssertionError("%s: %d of %d fp32 values out of tolerance; first at %d: got %r, expected %r"
                              % (what, bad.size, o.size, k, o[k], v[k]))
+
+
+# ---------------- fp32 reduction error bounds ----------------
+#
+# A sum of n terms accumulated in fp32 along a tree of depth d (the most
+# roundings any term goes through) is within gamma(d) * sum|terms| of the
+# exact sum, gamma(d) = d u / (1 - d u), u = 2^-24 (Higham, Accuracy and
+# Stability of Numerical Algorithms, 2nd ed., section 4.2). The RMSNorm
+# kernels' depths follow from their launch shapes, restated here from
+# dataflow_lib_amd/csrc/kernels/kernel_geometry.h and the kernels' loops.
+
+U32 = 2.0 ** -24
+RMS_CH, RMS_MAX_TPR, RMS_STREAM_TPR = 2, 1024, 256
+RMS_CELLS_PER_SLOT, RMS_INFLIGHT_BYTES = 64, 64 * 1024
+RMS_STREAM_WIDE_COLS, RMS_FIN_GROUPS = 4096, 256 // 16   # finish: RMS_FINISH_THREADS / RMS_FIN_COLS
+RMS_DW_SCRATCH_FLOATS = 4 << 20
+ELEM_BYTES = {FP32: 4, FP16: 2, BF16: 2}
+
+
+def gamma(d):
+    return d * U32 / (1.0 - d * U32)
+
+
+def rms_vec_chunks(n_cols, elem, aligned=True):
+    vec = 16 // elem
+    if n_cols <= 0 or n_cols % vec or not aligned:
+        return 0
+    nv = n_cols // vec
+    return nv if (nv + RMS_CH - 1) // RMS_CH <= RMS_MAX_TPR else 0
+
+
+def rms_tpr_for(nv):
+    if nv == 0:
+        return RMS_STREAM_TPR
+    t = (nv + RMS_CH - 1) // RMS_CH
+    return ((t + 63) // 64) * 64
+
+
+def rms_ws_depth(dt, n_cols, aligned=True):
+    """roundings along the weighted-sum tree of rms_norm's forward. Vector
+    path: four interleaved per-thread sums of RMS_CH * V / 4 terms each, added
+    pairwise (2), the wave's DPP tree (6), then the slot's waves in sequence.
+    Element path: a thread's terms in sequence, then the same. The first fma
+    of an fp32 sum rounds its product (bf16 / fp16 products are exact)."""
+    elem = ELEM_BYTES[dt]
+    nv = rms_vec_chunks(n_cols, elem, aligned)
+    tpr = rms_tpr_for(nv)
+    vec = 16 // elem
+    if nv:
+        per_thread = RMS_CH * vec // 4 + 2
+    elif aligned and n_cols % vec == 0:
+        per_thread = -(-(n_cols // vec) // tpr) * vec
+    else:
+        per_thread = -(-n_cols // tpr)
+    return per_thread + 6 + tpr // 64
+
+
+def rms_dw_depth(dt, n_rows, n_cols, arrays, cu_count, max_lds, aligned=True):
+    """roundings along the dW reduction of rms_norm_bwd_w (arrays = 2) and the
+    fused rms_norm_bwd (arrays = 3), for the launch shape rms_dw_geometry
+    picks: a thread's rows in sequence, the workgroup's slots in sequence,
+    then the finish pass (a thread's share of the grid's partial rows, its
+    RMS_FIN_GROUPS groups, then dW + the total). fp32 inputs add the rounding
+    of the product dY * X."""
+    elem = ELEM_BYTES[dt]
+    nv = rms_vec_chunks(n_cols, elem, aligned)
+    tpr = rms_tpr_for(nv) if nv else (RMS_MAX_TPR if n_cols >= RMS_STREAM_WIDE_COLS else RMS_STREAM_TPR)
+    per_slot = 2 * n_cols * elem * arrays
+    slots = min(max(1, min(RMS_INFLIGHT_BYTES // per_slot, 32)), max(1, RMS_MAX_TPR // tpr))
+    while slots >= 1:
+        colbuf = n_cols if nv else slots * n_cols
+        if (RMS_CELLS_PER_SLOT * slots + colbuf) * 4 <= max_lds:
+            break
+        slots -= 1
+    assert slots >= 1
+    grid = min(-(-n_rows // slots), cu_count, RMS_DW_SCRATCH_FLOATS // n_cols)
+    rows = -(-n_rows // (grid * slots))
+    finish = -(-grid // RMS_FIN_GROUPS) + RMS_FIN_GROUPS + 1
+    return rows + (slots - 1) + finish + (1 if dt == FP32 else 0)

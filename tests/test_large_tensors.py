@@ -10,7 +10,8 @@ buffer range, lands on different data and fails the comparison."""
 import numpy as np
 import pytest
 
-from support import BF16, NP_STORAGE, check_f32, check_rounded, normal, oracle, ptr, rng, to_storage
+from support import (BF16, NP_STORAGE, check_f32, check_rounded, gamma, normal, oracle, ptr, rms_ws_depth, rng,
+                     to_storage)
 
 pytestmark = pytest.mark.gpu
 
@@ -166,7 +167,7 @@ def test_rms_norm_past_4gib(hdl):
         gws = d.get(pws, (R,), np.float32)
         grs = d.get(prs, (R,), np.float32)
         check_f32(grs[:B], rs, what="rms_norm rstd")
-        check_f32(gws[:B], ws, floor=1e-6 * ws_abs, what="rms_norm weighted_sums")
+        check_f32(gws[:B], ws, floor=gamma(rms_ws_depth(dt, C)) * ws_abs, what="rms_norm weighted_sums")
         assert_blocks_equal(grs, B, "rms_norm rstd")
         assert_blocks_equal(gws, B, "rms_norm weighted_sums")
         y = d.get(py, (R, C), NP_STORAGE[dt])
