@@ -37,8 +37,9 @@ product's) moving the same
 total bytes (half read, half written), timed the same way - the ceiling the
 memory system offers that many bytes (the op's time over it is reported).
 
-cpu_baseline: the C oracle (oracle/liboracle.so, OpenMP over rows, fp64
-arithmetic) on a bounded row sample of the same ops, timed on this host.
+cpu_baseline: a C CPU implementation of the same math (oracle/libcpu_ref.so:
+fp32 arithmetic, fp64 reductions, OpenMP over rows, AVX-512) on the full
+configs, timed on this host's cores.
 """
 import argparse
 import ctypes
@@ -437,76 +438,103 @@ def time_head(h, hip, pool, api, iters):
             "vocab": V, "iters": iters, "note": "submit_transformer_head training pass; GEMMs on hipBLASLt"}
 
 
-def cpu_baseline(budget_s):
-    """Oracle (C, fp64, OpenMP over rows) on a row sample of the same ops."""
-    sys.path.insert(0, os.path.join(ROOT, "tests"))
-    from support import oracle, ptr
-    O = oracle()
-    g = np.random.default_rng(0)
-    rows = 512
-    T, D, F, V = rows, 4096, 14336, 128256
-    X = bf16_bits(g.standard_normal((T, D), dtype=np.float32))
-    W = bf16_bits(1 + 0.02 * g.standard_normal(D, dtype=np.float32))
-    dY = bf16_bits(g.standard_normal((T, D), dtype=np.float32))
-    dX = np.zeros((T, D), np.uint16)
-    Q = bf16_bits(g.standard_normal((T, 4096), dtype=np.float32))
-    K = bf16_bits(g.standard_normal((T, 1024), dtype=np.float32))
-    pos = (np.arange(T) % 2048).astype(np.int32)
-    G = bf16_bits(g.standard_normal((T, F), dtype=np.float32))
-    U = bf16_bits(g.standard_normal((T, F), dtype=np.float32))
-    DO = bf16_bits(g.standard_normal((T, F), dtype=np.float32))
-    ce_rows = 64
-    L = bf16_bits(2 * g.standard_normal((ce_rows, V), dtype=np.float32))
-    lab = g.integers(0, V, size=ce_rows).astype(np.uint32)
-    y, ws, rs, wa = np.empty((T, D)), np.empty(T), np.empty(T), np.empty(T)
-    rs32 = np.ones(T, np.float32)
-    dxp, dxf, dwp, dwa = np.empty((T, D)), np.empty((T, D)), np.empty(D), np.empty(D)
-    dW = np.zeros(D, np.float32)
-    qv, kv = np.empty((T, 4096)), np.empty((T, 1024))
-    so, dg, dgf, du = np.empty((T, F)), np.empty((T, F)), np.empty((T, F)), np.empty((T, F))
-    lo, hi, loss, mean = np.empty((ce_rows, V)), np.empty((ce_rows, V)), np.empty(ce_rows), np.zeros(1)
-    act = T * D * 2
-    work = [
-        ("rms_norm_fwd", 2 * act + D * 2 + 2 * T * 4, lambda: O.oracle_rms_norm(BF16, T, D, 1e-5, ptr(W), ptr(X), ptr(y), ptr(ws), ptr(rs), ptr(wa))),
-        ("rms_norm_bwd", 4 * act + D * 2 + T * 4 + 2 * D * 4, lambda: O.oracle_rms_norm_bwd(BF16, T, D, ptr(rs32), ptr(W), ptr(X), ptr(dY), ptr(dX), ptr(dW), ptr(dxp), ptr(dxf), ptr(dwp), ptr(dwa))),
-        ("rope_fwd", 2 * (Q.nbytes + K.nbytes) + T * 4, lambda: O.oracle_rope(BF16, 0, T * 4096, 4096, 128, 8, 500000, ptr(pos), ptr(Q), ptr(K), ptr(qv), ptr(kv))),
-        ("rope_bwd", 2 * (Q.nbytes + K.nbytes) + T * 4, lambda: O.oracle_rope(BF16, 1, T * 4096, 4096, 128, 8, 500000, ptr(pos), ptr(Q), ptr(K), ptr(qv), ptr(kv))),
-        ("swiglu_fwd", 3 * G.nbytes, lambda: O.oracle_swiglu(BF16, G.size, ptr(G), ptr(U), ptr(so))),
-        ("swiglu_bwd", 5 * G.nbytes, lambda: O.oracle_swiglu_bwd(BF16, G.size, ptr(G), ptr(U), ptr(DO), ptr(dg), ptr(dgf), ptr(du))),
-        ("softmax_xent_fused", 2 * L.nbytes + ce_rows * 8 + 4, lambda: O.oracle_softmax_cross_entropy(BF16, ce_rows, V, ptr(L), ptr(lab), ptr(lo), ptr(hi), ptr(loss), ptr(mean))),
-    ]
-    per, tot_b, tot_t = {}, 0, 0.0
-    t_start = time.perf_counter()
-    reps = 0
-    while True:
-        for name, nb, fn in work:
-            t0 = time.perf_counter()
-            assert fn() == 0
-            dt = time.perf_counter() - t0
-            e = per.setdefault(name, [0, 0.0])
-            e[0] += nb
-            e[1] += dt
-            tot_b += nb
-            tot_t += dt
-        reps += 1
-        if time.perf_counter() - t_start > budget_s or reps >= 1000:
-            break
-    model, flags = "", []
+def cpu_info():
+    """host CPU description from /proc/cpuinfo: full model name, family /
+    model / stepping numbers and the vector ISA flags that matter here"""
+    info = {"cpu_model": "", "cpu_family_model_stepping": "", "isa": []}
+    fam = mod = step = None
     try:
         with open("/proc/cpuinfo") as f:
             for line in f:
-                if line.startswith("model name") and not model:
-                    model = line.split(":", 1)[1].strip()
-                elif line.startswith("flags") and not flags:
-                    have = set(line.split(":", 1)[1].split())
-                    flags = [x for x in ("avx2", "fma", "avx512f", "avx512bw", "avx512_bf16", "avx512_fp16") if x in have]
+                k, _, v = line.partition(":")
+                k, v = k.strip(), v.strip()
+                if k == "model name" and not info["cpu_model"]:
+                    info["cpu_model"] = v
+                elif k == "cpu family" and fam is None:
+                    fam = v
+                elif k == "model" and mod is None:
+                    mod = v
+                elif k == "stepping" and step is None:
+                    step = v
+                elif k == "flags" and not info["isa"]:
+                    have = set(v.split())
+                    info["isa"] = [x for x in ("avx2", "fma", "avx512f", "avx512bw", "avx512vl", "avx512_bf16",
+                                               "avx512_fp16", "amx_bf16") if x in have]
     except OSError:
         pass
-    return {"value": round(tot_b / tot_t / 1e9, 3), "unit": "GB/s", "cores": int(O.oracle_num_threads()), "kind": "port",
-            "nproc": os.cpu_count(), "cpu_model": model, "isa": flags,
-            "sample": "oracle/liboracle.so (C, fp64, OpenMP over rows) on %d-row slices of configs 2-4 and %d rows of config 5, "
-                      "%d repetitions, same byte formulas" % (rows, ce_rows, reps),
-            "ops": {k: round(v[0] / v[1] / 1e9, 3) for k, v in per.items()}}
+    info["cpu_family_model_stepping"] = "%s/%s/%s" % (fam, mod, step)
+    return info
+
+
+def cpu_baseline(budget_s):
+    """oracle/libcpu_ref.so (C: bf16 storage, fp32 math, fp64 row and column
+    reductions, OpenMP over rows, AVX-512) on the FULL configs 2-5, timed on
+    this host: per op one warm-up, then the median of up to five runs (fewer
+    if `budget_s` runs out); GB/s from the same algorithmic byte formulas as
+    the GPU ops."""
+    L = ctypes.CDLL(os.path.join(ROOT, "oracle", "libcpu_ref.so"))
+    vp, i, f32, lg = ctypes.c_void_p, ctypes.c_int, ctypes.c_float, ctypes.c_long
+    L.cpu_ref_rms_norm_bf16.argtypes = [i, i, f32, vp, vp, vp, vp, vp]
+    L.cpu_ref_rms_norm_bwd_bf16.argtypes = [i, i, vp, vp, vp, vp, vp, vp]
+    L.cpu_ref_rope_bf16.argtypes = [i, lg, i, i, i, i, vp, vp, vp]
+    L.cpu_ref_swiglu_bf16.argtypes = [lg, vp, vp, vp]
+    L.cpu_ref_swiglu_bwd_bf16.argtypes = [lg, vp, vp, vp, vp, vp]
+    L.cpu_ref_softmax_xent_bf16.argtypes = [i, i, vp, vp, vp, vp]
+    g = np.random.default_rng(0)
+    block = bf16_bits(g.standard_normal(1 << 22, dtype=np.float32))
+
+    def tiled(n, scale=1.0, offset=0.0):
+        if scale == 1.0 and offset == 0.0:
+            return np.resize(block, n)
+        return np.resize(bf16_bits(offset + scale * (block.view(np.uint16).astype(np.uint32) << 16).view(np.float32)), n)
+
+    P = lambda a: a.ctypes.data_as(ctypes.c_void_p)
+    T, D, F, R, V = 8192, 4096, 14336, 4096, 128256
+    X, dY, dX = tiled(T * D), np.resize(block[::-1].copy(), T * D), np.zeros(T * D, np.uint16)
+    W = tiled(D, 0.02, 1.0)
+    Y, ws, rs, dW = np.empty(T * D, np.uint16), np.empty(T, np.float32), np.empty(T, np.float32), np.zeros(D, np.float32)
+    L.cpu_ref_rms_norm_bf16(T, D, 1e-5, P(W), P(X), P(Y), P(ws), P(rs))
+    Q, K, pos = tiled(T * 4096), tiled(T * 1024), (np.arange(T) % 2048).astype(np.int32)
+    G, U, DO = tiled(T * F), np.resize(block[1:], T * F), np.resize(block[2:], T * F)
+    SO, DG, DU = np.empty(T * F, np.uint16), np.empty(T * F, np.uint16), np.empty(T * F, np.uint16)
+    LG = tiled(R * V, 2.0)
+    lab = np.random.default_rng(9).integers(0, V, size=R).astype(np.uint32)
+    loss, mean = np.empty(R, np.float32), np.zeros(1, np.float32)
+    act = T * D * 2
+    work = [
+        ("rms_norm_fwd", 2 * act + D * 2 + 2 * T * 4, lambda: L.cpu_ref_rms_norm_bf16(T, D, 1e-5, P(W), P(X), P(Y), P(ws), P(rs))),
+        ("rms_norm_bwd", 4 * act + D * 2 + T * 4 + 2 * D * 4, lambda: L.cpu_ref_rms_norm_bwd_bf16(T, D, P(rs), P(W), P(X), P(dY), P(dX), P(dW))),
+        ("rope_fwd", 2 * (Q.nbytes + K.nbytes) + T * 4, lambda: L.cpu_ref_rope_bf16(0, T, 4096, 128, 8, 500000, P(pos), P(Q), P(K))),
+        ("rope_bwd", 2 * (Q.nbytes + K.nbytes) + T * 4, lambda: L.cpu_ref_rope_bf16(1, T, 4096, 128, 8, 500000, P(pos), P(Q), P(K))),
+        ("swiglu_fwd", 3 * G.nbytes, lambda: L.cpu_ref_swiglu_bf16(G.size, P(G), P(U), P(SO))),
+        ("swiglu_bwd", 5 * G.nbytes, lambda: L.cpu_ref_swiglu_bwd_bf16(G.size, P(G), P(U), P(DO), P(DG), P(DU))),
+        ("softmax_xent_fused", 2 * LG.nbytes + R * 8 + 4, lambda: L.cpu_ref_softmax_xent_bf16(R, V, P(LG), P(lab), P(loss), P(mean))),
+    ]
+    per, tot_b, tot_t = {}, 0, 0.0
+    per_op_budget = budget_s / len(work)
+    for name, nb, fn in work:
+        t0 = time.perf_counter()
+        fn()                                            # warm-up
+        first = time.perf_counter() - t0
+        runs = max(1, min(5, int(per_op_budget / max(first, 1e-6))))
+        times = []
+        for _ in range(runs):
+            t0 = time.perf_counter()
+            fn()
+            times.append(time.perf_counter() - t0)
+        med = sorted(times)[len(times) // 2]
+        per[name] = {"ms": round(med * 1e3, 2), "gbps": round(nb / med / 1e9, 2), "runs": runs}
+        tot_b += nb
+        tot_t += med
+    out = {"value": round(tot_b / tot_t / 1e9, 3), "unit": "GB/s", "cores": int(L.cpu_ref_threads()), "kind": "port",
+           "nproc": os.cpu_count(),
+           "sample": "oracle/libcpu_ref.so (C: bf16 storage, fp32 math, fp64 reductions, OpenMP over rows, "
+                     "gcc -O3 -march=x86-64-v4 -ffast-math) on the full configs 2-5 (rms_norm fwd+fused bwd 8192x4096, "
+                     "rope fwd+bwd 8192x(32+8)x128, swiglu fwd+bwd 8192x14336, fused softmax+xent 4096x128256); "
+                     "per op 1 warm-up + median of up to 5 runs; same byte formulas; value = total bytes / total time",
+           "ops": per}
+    out.update(cpu_info())
+    return out
 
 
 def load_traffic(name):
@@ -575,7 +603,7 @@ def main():
                 "frac": round(d["gbps"] / HBM_PEAK_GBPS, 4), "traffic": load_traffic(dom)}
     cpu = None
     if not args.no_cpu:
-        print("bench: CPU baseline (oracle) ~%.0f s" % args.cpu_budget, file=sys.stderr, flush=True)
+        print("bench: CPU baseline (oracle/libcpu_ref.so, full configs) ~%.0f s" % args.cpu_budget, file=sys.stderr, flush=True)
         cpu = cpu_baseline(args.cpu_budget)
     line = {
         "metric": "Achieved HBM GB/s and % of 8 TB/s peak per op at Llama-3-8B token shapes",

@@ -2,6 +2,10 @@
 
   oracle/liboracle.so    the C restatement (oracle.c) plus the CPU test backend
                          (cpu_backend.c), linked against the product's libdataflow.so
+  oracle/libcpu_ref.so   the CPU baseline bench.py times (cpu_ref.c: fp32 math, fp64
+                         reductions, OpenMP, AVX-512); built for x86-64-v4 rather
+                         than -march=native, since it is compiled in this container
+                         and runs on the GPU box's host (another x86 vendor)
   oracle/_ref/libref_host.so
                          the reference's own host C for the op registry, compiled
                          from its sources where they lie under /root/reference
@@ -17,6 +21,7 @@ HERE = os.path.dirname(os.path.abspath(__file__))
 ROOT = os.path.dirname(HERE)
 REF = os.environ.get("DATAFLOW_REFERENCE_ROOT", "/root/reference")
 ORACLE_OUT = os.path.join(HERE, "liboracle.so")
+CPU_REF_OUT = os.path.join(HERE, "libcpu_ref.so")
 REF_OUT = os.path.join(HERE, "_ref", "libref_host.so")
 PRODUCT_LIB = os.path.join(ROOT, "dataflow_lib_amd", "lib")
 
@@ -64,6 +69,16 @@ def build_oracle(verbose=False):
     return ORACLE_OUT
 
 
+def build_cpu_ref(verbose=False):
+    """The CPU baseline; -ffast-math lets expf vectorise (glibc's vector math
+    library), the counterpart of the GPU kernels' hardware exp2."""
+    tmp = CPU_REF_OUT + ".tmp%d" % os.getpid()
+    _run(["gcc", "-O3", "-march=x86-64-v4", "-ffast-math", "-fopenmp", "-fPIC", "-shared", "-std=gnu11",
+          os.path.join(HERE, "cpu_ref.c"), "-o", tmp, "-lm"], verbose)
+    os.replace(tmp, CPU_REF_OUT)
+    return CPU_REF_OUT
+
+
 def build_reference_host(verbose=False):
     """Returns the path of the built library, or None when the reference is absent."""
     if not all(os.path.exists(os.path.join(REF, s)) for s in REF_SOURCES):
@@ -86,4 +101,5 @@ def build_reference_host(verbose=False):
 if __name__ == "__main__":
     v = "-v" in sys.argv
     print(build_oracle(v))
+    print(build_cpu_ref(v))
     print(build_reference_host(v))

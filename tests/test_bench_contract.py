@@ -35,7 +35,8 @@ def test_cpu_baseline_object():
     assert "oracle" in cpu["sample"]
     assert cpu["nproc"] >= 1 and isinstance(cpu["cpu_model"], str) and isinstance(cpu["isa"], list)
     assert sorted(cpu["ops"]) == sorted(STEP_OPS)
-    assert all(v > 0 for v in cpu["ops"].values())
+    assert all(v["gbps"] > 0 and v["ms"] > 0 and v["runs"] >= 1 for v in cpu["ops"].values())
+    assert "full configs" in cpu["sample"] and cpu["cpu_family_model_stepping"]
 
 
 def test_traffic_figures_cover_the_step():
