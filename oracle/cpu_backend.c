@@ -58,8 +58,8 @@ static int cpu_register_native_code(Dataflow_Handle * h, char * code_filename, c
 
 static int cpu_submit_op(Dataflow_Handle * h, Op * op, int stream_id) {
 	if (stream_id < -1 || stream_id >= h->num_streams) {
-		fprintf(stderr, "Error: cannot submit op with nickname %s to stream id %d, when device only has %d streams. Null stream specified by -1...\n",
-				op->op_skeleton.header.op_nickname, stream_id, h->num_streams);
+		fprintf(stderr, "cpu backend: stream id %d (op %s) is out of range: %d streams, -1 for the null stream\n",
+				stream_id, op->op_skeleton.header.op_nickname, h->num_streams);
 		return -1;
 	}
 	Cpu_Function * f = NULL;

@@ -48,3 +48,13 @@ def test_traffic_figures_cover_the_step():
         assert t[op] > 0
     # the scales come from a copy of known size: FETCH_SIZE counts half the bytes, WRITE_SIZE all of them
     assert abs(t["fetch_scale"] - 2.0) < 0.01 and abs(t["write_scale"] - 1.0) < 0.01
+
+
+def test_cpu_baseline_library_keeps_the_process_float_mode():
+    """loading the CPU baseline (compiled with -ffast-math) must not switch the
+    process to flush-to-zero: the oracle tests in the same process rely on
+    subnormals"""
+    import ctypes
+    import numpy as np
+    ctypes.CDLL(os.path.join(ROOT, "oracle", "libcpu_ref.so"))
+    assert np.float32(1e-40) != 0 and np.float32(1e-40) * np.float32(2) == np.float32(2e-40)
