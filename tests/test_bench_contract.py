@@ -57,4 +57,5 @@ def test_cpu_baseline_library_keeps_the_process_float_mode():
     import ctypes
     import numpy as np
     ctypes.CDLL(os.path.join(ROOT, "oracle", "libcpu_ref.so"))
-    assert np.float32(1e-40) != 0 and np.float32(1e-40) * np.float32(2) == np.float32(2e-40)
+    tiny = np.float32(2.0 ** -140)                      # an fp32 subnormal, exactly representable
+    assert tiny != 0 and tiny * np.float32(2) == np.float32(2.0 ** -139)
