@@ -537,6 +537,20 @@ def cpu_baseline(budget_s):
     return out
 
 
+def host_submit_cost(api):
+    """microseconds per submit_* call from C (lib/bench_submit_cost): batches
+    of submits at the step's shapes, the queue drained between batches"""
+    import subprocess
+    exe = os.path.join(api.LIB_DIR, "bench_submit_cost")
+    if not os.path.exists(exe):
+        return None
+    r = subprocess.run([exe, api.KERNELS, api.CONFIG_LIB], capture_output=True, text=True, timeout=300)
+    if r.returncode != 0:
+        print("bench: submit-cost program failed (%d): %s" % (r.returncode, r.stderr[-500:]), file=sys.stderr)
+        return None
+    return json.loads(r.stdout.strip().splitlines()[-1])
+
+
 def load_traffic(name):
     path = os.path.join(ROOT, "profiles", "traffic.json")
     if not os.path.exists(path):
@@ -567,6 +581,9 @@ def main():
               file=sys.stderr)
         sys.exit(2)
     from dataflow_lib_amd import api
+    # host cost of the op API, timed from C in a child process started before
+    # this process makes its first HIP call
+    submit_us = host_submit_cost(api)
     hip = Hip()
     h = api.Handle(0, num_streams=1, matmul=not args.no_head)
     pool = Pool(h)
@@ -614,7 +631,8 @@ def main():
                                "swiglu fwd+bwd 8192x14336, fused softmax+xent 4096x128256",
                    "tokens": 8192, "hidden": 4096, "ffn": 14336, "vocab": 128256, "ce_rows": 4096},
         "pct_of_peak": round(100.0 * value / HBM_PEAK_GBPS, 1),
-        "ops": per_op, "extras": per_extra, "copy_reference": copy_ref, "transformer_head": head, "roofline": roofline,
+        "ops": per_op, "extras": per_extra, "copy_reference": copy_ref, "transformer_head": head,
+        "host_submit_us": submit_us, "roofline": roofline,
         "cpu_baseline": cpu,
         "device": dev,
         "wall_s_timed": round(wall, 3),

@@ -8,6 +8,7 @@ Outputs (in-tree, under dataflow_lib_amd/lib/):
   libdataflow_hipblaslt.so       the external matmul op on hipBLASLt (register_external_matmul)
   libdataflow_noalloc.so         the allocation-free entry point (include/dataflow_noalloc.h):
                                  host code and its gfx950 kernels in one HIP fat binary
+  bench_submit_cost              C program bench.py runs to time the host side of the op API
   bench_stream_copy_gfx950.hsaco streaming copies bench.py times as the memory system's
                                  ceiling (not part of the product; loaded by bench.py only)
 """
@@ -32,6 +33,7 @@ CONFIG_OUT = os.path.join(LIB, "libdataflow_hip_config.so")
 MATMUL_OUT = os.path.join(LIB, "libdataflow_hipblaslt.so")
 BENCH_COPY_OUT = os.path.join(LIB, "bench_stream_copy_gfx950.hsaco")
 NOALLOC_OUT = os.path.join(LIB, "libdataflow_noalloc.so")
+SUBMIT_COST_OUT = os.path.join(LIB, "bench_submit_cost")
 CXX = os.environ.get("CXX", "g++")
 
 C_FLAGS = ["-O2", "-fPIC", "-std=gnu11", "-Wall", "-Wextra", "-Wno-unused-parameter", "-Wno-stringop-truncation",
@@ -92,9 +94,11 @@ def build(verbose=False):
                                          "-I", INCLUDE, "-I", os.path.join(CSRC, "kernels"),
                                          os.path.join(CSRC, "noalloc", "rms_norm_bwd_noalloc.hip"), "-o", o,
                                          "-L", LIB, "-ldataflow", "-Wl,-rpath,$ORIGIN"], verbose))
+    _atomic(SUBMIT_COST_OUT, lambda o: _run([CC] + C_FLAGS + [os.path.join(CSRC, "bench", "submit_cost.c"), "-o", o,
+                                             "-L", LIB, "-ldataflow", "-Wl,-rpath,$ORIGIN"] + HIP_LINK, verbose))
     _atomic(BENCH_COPY_OUT, lambda o: _run([HIPCC] + HIP_FLAGS + [os.path.join(CSRC, "bench", "stream_copy.hip"), "-o", o], verbose))
     return {"kernels": KERNELS_OUT, "core": CORE_OUT, "config": CONFIG_OUT, "matmul": MATMUL_OUT,
-            "noalloc": NOALLOC_OUT, "bench_copy": BENCH_COPY_OUT}
+            "noalloc": NOALLOC_OUT, "bench_copy": BENCH_COPY_OUT, "submit_cost": SUBMIT_COST_OUT}
 
 
 if __name__ == "__main__":
