@@ -97,10 +97,26 @@ int rms_norm_set_launch_config(Hip_Launch_Config * hip_launch_config, Dataflow_H
 	return 0;
 }
 
+static int is_fp8(Hip_Function * f, int i) {
+	const DataflowDatatype dt = f->op_skeleton.header.arg_dtypes[i];
+	return dt == DATAFLOW_FP8E4M3 || dt == DATAFLOW_FP8E5M2;
+}
+
+/* fp8 x 16-bit variants (fp8_ops.hip): one 256-thread workgroup per row at a
+ * time, eight elements per lane, four workgroups per CU */
+static void rms_fp8_rowwise(Hip_Launch_Config * c, Dataflow_Handle * h, int n_rows, int n_cols) {
+	const long grid = (n_cols == 0) ? 0 : MY_MIN((long) n_rows, (long) dev(h)->cu_count * 4);
+	set_1d(c, (unsigned) grid, 256, 0);
+}
+
 int rms_norm_bwd_x_set_launch_config(Hip_Launch_Config * hip_launch_config, Dataflow_Handle * dataflow_handle, Hip_Function * hip_function, Op * op) {
 	const int n_rows = ARG(op, 0, int), n_cols = ARG(op, 1, int);
 	const size_t elem = arg_elem_bytes(hip_function, 5);
 	if (rms_check("rms norm bwd x", n_rows, n_cols, elem)) return -1;
+	if (is_fp8(hip_function, 5)) {
+		rms_fp8_rowwise(hip_launch_config, dataflow_handle, n_rows, n_cols);
+		return 0;
+	}
 	const int nv = rms_vec_chunks(n_cols, (int) elem, ptr_bits(ARG(op, 5, void *)) | ptr_bits(ARG(op, 6, void *)) |
 													ptr_bits(ARG(op, 7, void *)) | ptr_bits(ARG(op, 8, void *)));
 	rms_rowwise(hip_launch_config, dataflow_handle, hip_function, (n_cols == 0) ? 0 : n_rows, n_cols, elem, nv, 3);
@@ -143,6 +159,25 @@ int rms_norm_bwd_w_set_launch_config(Hip_Launch_Config * hip_launch_config, Data
 	const int n_rows = ARG(op, 0, int), n_cols = ARG(op, 1, int);
 	const size_t elem = arg_elem_bytes(hip_function, 4);
 	if (rms_check("rms norm bwd w", n_rows, n_cols, elem)) return -1;
+	if (is_fp8(hip_function, 4)) {
+		/* fp8 X: one 256-thread workgroup per CU, each summing its rows into an
+		 * LDS row of n_cols floats, one partial row per workgroup */
+		if (n_rows == 0 || n_cols == 0) {
+			set_1d(hip_launch_config, 0, 1, 0);
+			return 0;
+		}
+		const long lds = (long) n_cols * (long) sizeof(float);
+		const long max_lds = hip_function->function_config.func_max_smem > 0 ? hip_function->function_config.func_max_smem
+																		   : dev(dataflow_handle)->max_smem_per_block;
+		if (lds > max_lds || n_cols > (long) RMS_DW_SCRATCH_FLOATS) {
+			fprintf(stderr, "Error: rms norm bwd w: rows of %d columns need more LDS than the %ld bytes available...\n", n_cols, max_lds);
+			return -1;
+		}
+		long grid = MY_MIN((long) n_rows, (long) dev(dataflow_handle)->cu_count);
+		grid = MY_MIN(grid, (long) RMS_DW_SCRATCH_FLOATS / (long) n_cols);
+		set_1d(hip_launch_config, (unsigned) grid, 256, (unsigned) lds);
+		return 0;
+	}
 	const int nv = rms_vec_chunks(n_cols, (int) elem, ptr_bits(ARG(op, 4, void *)) | ptr_bits(ARG(op, 5, void *)));
 	return rms_dw_config(hip_launch_config, dataflow_handle, hip_function, "rms norm bwd w", n_rows, n_cols, elem, nv, 2);
 }

@@ -170,10 +170,13 @@ DEFINE_FWD_SETTER(set_native_rope_copy_to_seq_context_skeleton, "rope_copy_to_se
 
 /* ---- registration ---- */
 
-/* Variants provided by the gfx950 code object. The reference's fp8 variants
- * of the arithmetic ops are absent (submit_op reports them as unknown
- * fingerprints); embedding and copy_to_seq_context move bytes only, so they
- * come in every storage type the reference registers, fp8 included. */
+/* Variants provided by the gfx950 code object: the reference's 54
+ * (set_native_op_skeletons.c:5-200: fp32 / fp16 / bf16 / fp8e4m3 / fp8e5m2
+ * forward ops, fp32 / fp16 / bf16 rope_bwd_x and cross_entropy_loss, and the
+ * seven (forward, backward) type pairs of the backward ops and softmax,
+ * fp8 forward with fp16 / bf16 backward among them), copy_to_seq_context in
+ * all five storage types, and the three fused ops this library adds in fp32 /
+ * fp16 / bf16. */
 typedef struct { const char * op; DataflowDatatype fwd; DataflowDatatype bwd; } Native_Variant;
 
 #define FWD3(op) {op, DATAFLOW_FP32, DATAFLOW_NONE}, {op, DATAFLOW_FP16, DATAFLOW_NONE}, {op, DATAFLOW_BF16, DATAFLOW_NONE}
@@ -181,19 +184,22 @@ typedef struct { const char * op; DataflowDatatype fwd; DataflowDatatype bwd; } 
 #define PAIR3(op) {op, DATAFLOW_FP32, DATAFLOW_FP32}, {op, DATAFLOW_FP16, DATAFLOW_FP16}, {op, DATAFLOW_BF16, DATAFLOW_BF16}
 
 #define FWD5(op) FWD3(op), {op, DATAFLOW_FP8E4M3, DATAFLOW_NONE}, {op, DATAFLOW_FP8E5M2, DATAFLOW_NONE}
+/* the reference's seven (fwd, bwd) pairs: the three same-type ones and fp8 x {fp16, bf16} */
+#define PAIR7(op) PAIR3(op), {op, DATAFLOW_FP8E4M3, DATAFLOW_FP16}, {op, DATAFLOW_FP8E4M3, DATAFLOW_BF16}, \
+				  {op, DATAFLOW_FP8E5M2, DATAFLOW_FP16}, {op, DATAFLOW_FP8E5M2, DATAFLOW_BF16}
 
 static const Native_Variant native_variants[] = {
 	FWD5("embedding"),
-	FWD3("rms_norm"),
-	PAIR3("rms_norm_bwd_x"),
-	PAIR3("rms_norm_bwd_w"),
+	FWD5("rms_norm"),
+	PAIR7("rms_norm_bwd_x"),
+	PAIR7("rms_norm_bwd_w"),
 	PAIR3("rms_norm_bwd"),
-	FWD3("rope"),
+	FWD5("rope"),
 	BWD3("rope_bwd_x"),
 	FWD5("copy_to_seq_context"),
-	FWD3("swiglu"),
-	PAIR3("swiglu_bwd_x"),
-	PAIR3("softmax"),
+	FWD5("swiglu"),
+	PAIR7("swiglu_bwd_x"),
+	PAIR7("softmax"),
 	BWD3("cross_entropy_loss"),
 	FWD3("softmax_cross_entropy_loss"),
 	FWD3("rope_copy_to_seq_context"),

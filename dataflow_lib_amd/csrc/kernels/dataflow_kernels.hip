@@ -8,3 +8,4 @@
 #include "swiglu.hip"
 #include "softmax_xent.hip"
 #include "gather_scatter.hip"
+#include "fp8_ops.hip"

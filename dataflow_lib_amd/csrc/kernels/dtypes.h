@@ -87,6 +87,110 @@ template <> __device__ __forceinline__ R16 pack16<f16_t>(const float * f) {
 }
 
 /*
+ * fp8 storage: the OCP 8-bit formats E4M3 (bias 7, no infinities, max 448)
+ * and E5M2 (bias 15, max 57344), which gfx950's conversion instructions
+ * implement (v_cvt_f32_fp8 / _bf8 decode, v_cvt_pk_fp8_f32 / _bf8_f32 encode
+ * two floats with round to nearest even). Encoding saturates to the largest
+ * finite value, as the reference's conversions do (CUDA's fp8 constructors
+ * from float, __NV_SATFINITE): the input is clamped to +-max first, NaN kept.
+ * fp8 is a forward-only storage type.
+ */
+struct fp8e4m3_t { uint8_t bits; };
+struct fp8e5m2_t { uint8_t bits; };
+
+__device__ __forceinline__ float to_f(fp8e4m3_t x) { return __builtin_amdgcn_cvt_f32_fp8((int) x.bits, 0); }
+__device__ __forceinline__ float to_f(fp8e5m2_t x) { return __builtin_amdgcn_cvt_f32_bf8((int) x.bits, 0); }
+
+template <typename T> struct Fp8Traits;
+template <> struct Fp8Traits<fp8e4m3_t> {
+	static constexpr float MAX = 448.0f;
+	/* two floats into bytes 0-1 (hi = false) or 2-3 (hi = true) of `old` */
+	__device__ static __forceinline__ uint32_t cvt_pk(float a, float b, uint32_t old, bool hi) {
+		return hi ? (uint32_t) __builtin_amdgcn_cvt_pk_fp8_f32(a, b, (int) old, true)
+				  : (uint32_t) __builtin_amdgcn_cvt_pk_fp8_f32(a, b, (int) old, false);
+	}
+	__device__ static __forceinline__ float byte(uint32_t w, int k) {
+		switch (k) {
+			case 0: return __builtin_amdgcn_cvt_f32_fp8((int) w, 0);
+			case 1: return __builtin_amdgcn_cvt_f32_fp8((int) w, 1);
+			case 2: return __builtin_amdgcn_cvt_f32_fp8((int) w, 2);
+			default: return __builtin_amdgcn_cvt_f32_fp8((int) w, 3);
+		}
+	}
+};
+template <> struct Fp8Traits<fp8e5m2_t> {
+	static constexpr float MAX = 57344.0f;
+	__device__ static __forceinline__ uint32_t cvt_pk(float a, float b, uint32_t old, bool hi) {
+		return hi ? (uint32_t) __builtin_amdgcn_cvt_pk_bf8_f32(a, b, (int) old, true)
+				  : (uint32_t) __builtin_amdgcn_cvt_pk_bf8_f32(a, b, (int) old, false);
+	}
+	__device__ static __forceinline__ float byte(uint32_t w, int k) {
+		switch (k) {
+			case 0: return __builtin_amdgcn_cvt_f32_bf8((int) w, 0);
+			case 1: return __builtin_amdgcn_cvt_f32_bf8((int) w, 1);
+			case 2: return __builtin_amdgcn_cvt_f32_bf8((int) w, 2);
+			default: return __builtin_amdgcn_cvt_f32_bf8((int) w, 3);
+		}
+	}
+};
+
+/* clamp to +-max, NaN kept (the saturating conversion's range) */
+template <typename T>
+__device__ __forceinline__ float fp8_sat(float f) {
+	const float m = Fp8Traits<T>::MAX;
+	return (f != f) ? f : __builtin_fminf(__builtin_fmaxf(f, -m), m);
+}
+/* four floats into one word, byte k = element k */
+template <typename T>
+__device__ __forceinline__ uint32_t fp8_pack4(float a, float b, float c, float d) {
+	const uint32_t lo = Fp8Traits<T>::cvt_pk(fp8_sat<T>(a), fp8_sat<T>(b), 0u, false);
+	return Fp8Traits<T>::cvt_pk(fp8_sat<T>(c), fp8_sat<T>(d), lo, true);
+}
+template <typename T>
+__device__ __forceinline__ void fp8_unpack4(uint32_t w, float * f) {
+#pragma unroll
+	for (int k = 0; k < 4; k++) f[k] = Fp8Traits<T>::byte(w, k);
+}
+
+template <> __device__ __forceinline__ fp8e4m3_t from_f<fp8e4m3_t>(float f) {
+	return fp8e4m3_t{(uint8_t) (fp8_pack4<fp8e4m3_t>(f, 0.0f, 0.0f, 0.0f) & 0xffu)};
+}
+template <> __device__ __forceinline__ fp8e5m2_t from_f<fp8e5m2_t>(float f) {
+	return fp8e5m2_t{(uint8_t) (fp8_pack4<fp8e5m2_t>(f, 0.0f, 0.0f, 0.0f) & 0xffu)};
+}
+
+template <> __device__ __forceinline__ void unpack16<fp8e4m3_t>(const R16 & r, float * f) {
+#pragma unroll
+	for (int i = 0; i < 4; i++) fp8_unpack4<fp8e4m3_t>(r.w[i], f + 4 * i);
+}
+template <> __device__ __forceinline__ void unpack16<fp8e5m2_t>(const R16 & r, float * f) {
+#pragma unroll
+	for (int i = 0; i < 4; i++) fp8_unpack4<fp8e5m2_t>(r.w[i], f + 4 * i);
+}
+template <> __device__ __forceinline__ R16 pack16<fp8e4m3_t>(const float * f) {
+	R16 r;
+#pragma unroll
+	for (int i = 0; i < 4; i++) r.w[i] = fp8_pack4<fp8e4m3_t>(f[4 * i], f[4 * i + 1], f[4 * i + 2], f[4 * i + 3]);
+	return r;
+}
+template <> __device__ __forceinline__ R16 pack16<fp8e5m2_t>(const float * f) {
+	R16 r;
+#pragma unroll
+	for (int i = 0; i < 4; i++) r.w[i] = fp8_pack4<fp8e5m2_t>(f[4 * i], f[4 * i + 1], f[4 * i + 2], f[4 * i + 3]);
+	return r;
+}
+
+/* 8 bytes: eight fp8 elements, or the fp8 half of a mixed fp8 x 16-bit chunk */
+struct __attribute__((aligned(8))) R8 {
+	uint32_t w[2];
+};
+template <typename T>
+__device__ __forceinline__ void unpack8_fp8(const R8 & r, float * f) {
+	fp8_unpack4<T>(r.w[0], f);
+	fp8_unpack4<T>(r.w[1], f + 4);
+}
+
+/*
  * A "chunk" is V consecutive elements handled by one lane: V = VecOf<T>::N
  * (one 16-byte access) on the vector path, V = 1 on the element path used
  * for unaligned or ragged rows. raw_t is what sits in registers.

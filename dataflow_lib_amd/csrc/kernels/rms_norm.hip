@@ -47,3 +47,17 @@ __device__ int g_rms_dw_nparts;
 RMS_KERNELS(fp32, fp32_fp32, float)
 RMS_KERNELS(fp16, fp16_fp16, f16_t)
 RMS_KERNELS(bf16, bf16_bf16, bf16_t)
+
+/* fp8 forward (reference: rms_norm.cu:415-659): out = fp8((x * rstd) * w);
+ * the statistic slot receives sum_j x^2 instead of rstd and weighted_sums is
+ * not written, as in the reference's fp8 kernels */
+#define RMS_FP8_FWD_KERNEL(FSUF, T)                                                                                     \
+	extern "C" __global__ void __launch_bounds__(1024) rms_norm_##FSUF##_kernel(int n_rows, int n_cols, float eps,       \
+			T * rms_weight, T * X, T * out, float * weighted_sums, float * sq_sums) {                                   \
+		RmsArgs a = {n_rows, n_cols, eps, nullptr, nullptr, nullptr, sq_sums, rms_weight, X, nullptr, out, nullptr,      \
+					 nullptr, nullptr, true};                                                                            \
+		rms_run<T, T, RMS_FWD>(a);                                                                                       \
+	}
+
+RMS_FP8_FWD_KERNEL(fp8e4m3, fp8e4m3_t)
+RMS_FP8_FWD_KERNEL(fp8e5m2, fp8e5m2_t)

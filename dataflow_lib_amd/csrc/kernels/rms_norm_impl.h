@@ -58,6 +58,7 @@ struct RmsArgs {
 	void * dW;                /* bwd_w: T; bwd: fp32 */
 	float * partials;         /* dW modes: one fp32 partial row per workgroup */
 	int * nparts_out;         /* dW modes, optional: receives the grid size */
+	bool sq_stat;             /* fwd: rs_out receives sum_j x^2 instead of rstd (the fp8 kernels) */
 };
 
 /* sums of (a, b) over the waves of this thread's slot, one barrier.
@@ -191,7 +192,7 @@ __device__ __forceinline__ void rms_vector(const RmsArgs & a, int nv, float * ld
 			const float r = 1.0f / sqrtf(ss / (float) n_cols + a.eps);
 			if (live && tr == 0) {
 				if (a.ws_out) a.ws_out[row] = sw;
-				if (a.rs_out) a.rs_out[row] = r;
+				if (a.rs_out) a.rs_out[row] = a.sq_stat ? ss : r;
 			}
 #pragma unroll
 			for (int c = 0; c < RMS_CH; c++) {
@@ -344,7 +345,7 @@ __device__ __forceinline__ void rms_stream(const RmsArgs & a, float * lds) {
 				const float r = 1.0f / sqrtf(ss / (float) n_cols + a.eps);
 				if (tr == 0) {
 					if (a.ws_out) a.ws_out[row] = sw;
-					if (a.rs_out) a.rs_out[row] = r;
+					if (a.rs_out) a.rs_out[row] = a.sq_stat ? ss : r;
 				}
 				if (vec) {
 					for (int c = tr; c < nv; c += tpr) {

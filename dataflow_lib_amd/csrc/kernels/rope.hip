@@ -386,3 +386,13 @@ ROPE_KERNELS(bf16, bf16_t)
 ROPE_KV_KERNELS(fp32, float)
 ROPE_KV_KERNELS(fp16, f16_t)
 ROPE_KV_KERNELS(bf16, bf16_t)
+
+/* fp8 forward only (reference: rope.cu:183-300; rope_bwd_x has no fp8 kernels) */
+#define ROPE_FP8_KERNEL(SUFFIX, T)                                                                                  \
+	extern "C" __global__ void __launch_bounds__(256) rope_##SUFFIX##_kernel(uint64_t N, int model_dim, int head_dim, \
+			int num_kv_heads, int theta, int * seq_positions, T * X_q, T * X_k) {                                    \
+		rope_dispatch<T, false>(N, model_dim, head_dim, num_kv_heads, theta, seq_positions, X_q, X_k);              \
+	}
+
+ROPE_FP8_KERNEL(fp8e4m3, fp8e4m3_t)
+ROPE_FP8_KERNEL(fp8e5m2, fp8e5m2_t)

@@ -167,3 +167,14 @@ __device__ __forceinline__ void swiglu_bwd(long n, const T * g, const T * u, con
 SWIGLU_KERNELS(fp32, fp32_fp32, float)
 SWIGLU_KERNELS(fp16, fp16_fp16, f16_t)
 SWIGLU_KERNELS(bf16, bf16_bf16, bf16_t)
+
+/* fp8 forward (reference: swiglu.cu:70-114); the fp8 x fp16/bf16 backward
+ * is in fp8_ops.hip */
+#define SWIGLU_FP8_KERNEL(SUFFIX, T)                                                                                 \
+	extern "C" __global__ void __launch_bounds__(512) swiglu_##SUFFIX##_kernel(int num_rows, int num_cols,          \
+			T * x_w1, T * x_w3, T * out) {                                                                           \
+		swiglu_fwd<T>((long) num_rows * (long) num_cols, x_w1, x_w3, out);                                           \
+	}
+
+SWIGLU_FP8_KERNEL(fp8e4m3, fp8e4m3_t)
+SWIGLU_FP8_KERNEL(fp8e5m2, fp8e5m2_t)

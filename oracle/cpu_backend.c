@@ -280,3 +280,81 @@ ADAPT_MOVE(fp8e5m2, 1)
 ADAPT_DT(fp32, fp32_fp32, ORACLE_FP32, ORACLE_FP32_BYTES)
 ADAPT_DT(fp16, fp16_fp16, ORACLE_FP16, ORACLE_FP16_BYTES)
 ADAPT_DT(bf16, bf16_bf16, ORACLE_BF16, ORACLE_BF16_BYTES)
+
+/* ---- fp8 forward types (OCP E4M3 / E5M2) ---- */
+
+/* the fp8 forward writes sum_j x^2 into the statistic slot and leaves
+ * weighted_sums alone (rms_norm.cu:415-659) */
+static int rms_norm_fp8_adapter(int dt, void ** op_args) {
+	const int n_rows = A(0, int), n_cols = A(1, int);
+	float * ss_out = A(7, float *);
+	const long n = (long) n_rows * n_cols;
+	double * y = dbuf(n), * ss = dbuf(n_rows);
+	int ret = oracle_rms_norm(dt, n_rows, n_cols, A(2, float), A(3, void *), A(4, void *), y, NULL, NULL, NULL);
+	if (!ret) ret = oracle_rms_norm_sq_sums(dt, n_rows, n_cols, A(4, void *), ss);
+	if (!ret) {
+		oracle_store(dt, y, n, A(5, void *));
+		for (int i = 0; i < n_rows; i++) if (ss_out) ss_out[i] = (float) ss[i];
+	}
+	free(y); free(ss);
+	return ret;
+}
+
+static int rms_norm_bwd_x2_adapter(int fdt, int bdt, void ** op_args) {
+	const int n_rows = A(0, int), n_cols = A(1, int);
+	const long n = (long) n_rows * n_cols;
+	double * v = dbuf(n);
+	int ret = oracle_rms_norm_bwd_x2_exact(fdt, bdt, n_rows, n_cols, A(3, float *), A(4, float *), A(5, void *), A(6, void *),
+											A(7, void *), A(8, void *), v);
+	if (!ret) oracle_store(bdt, v, n, A(8, void *));
+	free(v);
+	return ret;
+}
+
+static int rms_norm_bwd_w2_adapter(int fdt, int bdt, void ** op_args) {
+	const int n_rows = A(0, int), n_cols = A(1, int);
+	double * v = dbuf(n_cols);
+	int ret = oracle_rms_norm_bwd_w2(fdt, bdt, bdt, n_rows, n_cols, A(3, float *), A(4, void *), A(5, void *), A(6, void *), v, NULL);
+	if (!ret) oracle_store(bdt, v, n_cols, A(6, void *));
+	free(v);
+	return ret;
+}
+
+static int swiglu_bwd2_adapter(int fdt, int bdt, void ** op_args) {
+	const long n = (long) A(0, int) * A(1, int);
+	double * dg = dbuf(n), * du = dbuf(n);
+	int ret = oracle_swiglu_bwd2(fdt, bdt, n, A(2, void *), A(3, void *), A(4, void *), dg, NULL, du);
+	if (!ret) {
+		oracle_store(bdt, dg, n, A(5, void *));
+		oracle_store(bdt, du, n, A(6, void *));
+	}
+	free(dg); free(du);
+	return ret;
+}
+
+static int softmax2_adapter(int fdt, int bdt, void ** op_args) {
+	const int n_rows = A(0, int), n_cols = A(1, int);
+	const long n = (long) n_rows * n_cols;
+	double * y = dbuf(n);
+	int ret = oracle_softmax(fdt, bdt, n_rows, n_cols, A(2, void *), y);
+	if (!ret) oracle_store(bdt, y, n, A(3, void *));
+	free(y);
+	return ret;
+}
+
+#define ADAPT_FP8(sfx, code)                                                                                    \
+	int rms_norm_##sfx##_kernel(void ** a) { return rms_norm_fp8_adapter(code, a); }                            \
+	int rope_##sfx##_kernel(void ** a) { return rope_adapter(code, 0, a); }                                     \
+	int swiglu_##sfx##_kernel(void ** a) { return swiglu_adapter(code, a); }
+#define ADAPT_FP8_PAIR(pair, fcode, bcode)                                                                      \
+	int rms_norm_bwd_x_##pair##_kernel(void ** a) { return rms_norm_bwd_x2_adapter(fcode, bcode, a); }          \
+	int rms_norm_bwd_w_##pair##_kernel(void ** a) { return rms_norm_bwd_w2_adapter(fcode, bcode, a); }          \
+	int swiglu_bwd_x_##pair##_kernel(void ** a) { return swiglu_bwd2_adapter(fcode, bcode, a); }                \
+	int softmax_##pair##_kernel(void ** a) { return softmax2_adapter(fcode, bcode, a); }
+
+ADAPT_FP8(fp8e4m3, ORACLE_FP8E4M3)
+ADAPT_FP8(fp8e5m2, ORACLE_FP8E5M2)
+ADAPT_FP8_PAIR(fp8e4m3_fp16, ORACLE_FP8E4M3, ORACLE_FP16)
+ADAPT_FP8_PAIR(fp8e4m3_bf16, ORACLE_FP8E4M3, ORACLE_BF16)
+ADAPT_FP8_PAIR(fp8e5m2_fp16, ORACLE_FP8E5M2, ORACLE_FP16)
+ADAPT_FP8_PAIR(fp8e5m2_bf16, ORACLE_FP8E5M2, ORACLE_BF16)

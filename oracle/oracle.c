@@ -27,28 +27,73 @@ int oracle_num_threads(void) {
 
 /* ---------------- formats ---------------- */
 
+/* mantissa bits (implicit bit included), minimum normal exponent and
+ * largest finite value. fp8: the OCP 8-bit formats (OCP 8-bit Floating Point
+ * Specification, OFP8, rev. 1.0): E4M3 (bias 7, no infinities, S.1111.111 is
+ * NaN, max 448) and E5M2 (bias 15, IEEE-style infinities and NaNs, max 57344) */
 static int fmt(int dt, int * mant, int * emin, double * maxf) {
 	switch (dt) {
 		case ORACLE_FP32: *mant = 24; *emin = -126; *maxf = ldexp(2.0 - ldexp(1.0, -23), 127); return 0;
 		case ORACLE_FP16: *mant = 11; *emin = -14;  *maxf = 65504.0; return 0;
 		case ORACLE_BF16: *mant = 8;  *emin = -126; *maxf = ldexp(2.0 - ldexp(1.0, -7), 127); return 0;
+		case ORACLE_FP8E4M3: *mant = 4; *emin = -6; *maxf = 448.0; return 0;
+		case ORACLE_FP8E5M2: *mant = 3; *emin = -14; *maxf = 57344.0; return 0;
 		default: return -1;
 	}
 }
 
-/* round-to-nearest-even of v into the format, subnormals included */
+static int is_fp8(int dt) { return dt == ORACLE_FP8E4M3 || dt == ORACLE_FP8E5M2; }
+
+/* round-to-nearest-even of v into the format, subnormals included. Overflow
+ * gives infinity, except for the fp8 formats, whose conversions saturate to
+ * the largest finite value (infinite inputs too): the reference converts to
+ * fp8 through the __nv_fp8_e4m3 / __nv_fp8_e5m2 constructors from float, which
+ * saturate to finite (the CUDA fp8 types' documented __NV_SATFINITE mode). */
 double oracle_round(double v, int dt) {
 	int mant, emin;
 	double maxf;
-	if (fmt(dt, &mant, &emin, &maxf) || v == 0.0 || !isfinite(v)) return v;
+	if (fmt(dt, &mant, &emin, &maxf) || v == 0.0 || isnan(v)) return v;
+	if (isinf(v)) return is_fp8(dt) ? copysign(maxf, v) : v;
 	int e;
 	frexp(v, &e);                      /* |v| in [2^(e-1), 2^e) */
 	int lead = e - 1;
 	if (lead < emin) lead = emin;
 	const int q = lead - (mant - 1);   /* quantum exponent */
 	double r = ldexp(nearbyint(ldexp(v, -q)), q);   /* default mode: ties to even */
-	if (fabs(r) > maxf) r = copysign(INFINITY, v);
+	if (fabs(r) > maxf) r = is_fp8(dt) ? copysign(maxf, v) : copysign(INFINITY, v);
 	return r;
+}
+
+/* value of an fp8 code */
+static double fp8_decode(int dt, uint8_t b) {
+	const int s = b >> 7;
+	double v;
+	if (dt == ORACLE_FP8E4M3) {
+		const int e = (b >> 3) & 15, m = b & 7;
+		if (e == 15 && m == 7) return NAN;
+		v = (e == 0) ? ldexp((double) m, -9) : ldexp((double) (8 + m), e - 10);
+	}
+	else {
+		const int e = (b >> 2) & 31, m = b & 3;
+		if (e == 31) return m ? NAN : (s ? -INFINITY : INFINITY);
+		v = (e == 0) ? ldexp((double) m, -16) : ldexp((double) (4 + m), e - 17);
+	}
+	return s ? -v : v;
+}
+
+/* code of a value already representable in the fp8 format (NaN -> 0x7f) */
+static uint8_t fp8_encode_exact(int dt, double r) {
+	if (isnan(r)) return 0x7f;
+	const uint8_t s = signbit(r) ? 0x80 : 0;
+	const double a = fabs(r);
+	if (dt == ORACLE_FP8E5M2 && isinf(r)) return (uint8_t) (s | 0x7c);
+	const int mbits = (dt == ORACLE_FP8E4M3) ? 3 : 2;
+	const int bias = (dt == ORACLE_FP8E4M3) ? 7 : 15;
+	if (a < ldexp(1.0, 1 - bias)) return (uint8_t) (s | (uint8_t) ldexp(a, bias - 1 + mbits));   /* subnormal or zero */
+	int e;
+	const double f = frexp(a, &e);     /* a = f * 2^e, f in [0.5, 1) */
+	const int m = (int) ldexp(f, mbits + 1) - (1 << mbits);
+	return (uint8_t) (s | (uint8_t) ((e - 1 + bias) << mbits) | (uint8_t) m);
 }
 
 /* spacing of the format at |v| (the ulp of v's binade) */
@@ -82,6 +127,9 @@ static double load1(int dt, const void * p, long i) {
 			else v = ldexp((double) (m + 1024), e - 25);
 			return s ? -v : v;
 		}
+		case ORACLE_FP8E4M3:
+		case ORACLE_FP8E5M2:
+			return fp8_decode(dt, ((const uint8_t *) p)[i]);
 		default: return NAN;
 	}
 }
@@ -120,6 +168,10 @@ static void store1(int dt, void * p, long i, double v) {
 			((uint16_t *) p)[i] = out;
 			break;
 		}
+		case ORACLE_FP8E4M3:
+		case ORACLE_FP8E5M2:
+			((uint8_t *) p)[i] = fp8_encode_exact(dt, r);
+			break;
 		default: break;
 	}
 }
@@ -132,7 +184,9 @@ void oracle_store(int dt, const double * src, long n, void * dst) {
 	for (long i = 0; i < n; i++) store1(dt, dst, i, src[i]);
 }
 
-static int dt_ok(int dt) { return dt == ORACLE_FP32 || dt == ORACLE_FP16 || dt == ORACLE_BF16; }
+static int dt_ok(int dt) { return dt == ORACLE_FP32 || dt == ORACLE_FP16 || dt == ORACLE_BF16 || is_fp8(dt); }
+/* storage types of the backward tensors (fp8 is a forward-only type) */
+static int bwd_dt_ok(int dt) { return dt == ORACLE_FP32 || dt == ORACLE_FP16 || dt == ORACLE_BF16; }
 
 /* ---------------- RMSNorm ---------------- */
 
@@ -162,20 +216,37 @@ int oracle_rms_norm(int dt, int n_rows, int n_cols, float eps, const void * W, c
 	return 0;
 }
 
-/* reference: src/ops/nvidia/norm/rms_norm_bwd_x.cu:175-256 (bf16), :4-86 (fp32):
+/* the fp8 forward kernels write sum_j x^2 per row where the others write
+ * rstd (src/ops/nvidia/norm/rms_norm.cu:511,635) */
+int oracle_rms_norm_sq_sums(int dt, int n_rows, int n_cols, const void * X, double * sq_sums) {
+	if (!dt_ok(dt) || n_rows < 0 || n_cols <= 0) return -1;
+	#pragma omp parallel for schedule(static)
+	for (int r = 0; r < n_rows; r++) {
+		double ss = 0.0;
+		for (int j = 0; j < n_cols; j++) {
+			const double x = load1(dt, X, (long) r * n_cols + j);
+			ss += x * x;
+		}
+		sq_sums[r] = ss;
+	}
+	return 0;
+}
+
+/* reference: src/ops/nvidia/norm/rms_norm_bwd_x.cu:175-256 (bf16), :4-86 (fp32),
+ * :259-590 (fp8 W and X, fp16 / bf16 dY and dX):
  *   deriv = w*r - ((x*r^3)/n)*ws;  dX = rnd(dX + rnd(dY * rnd(deriv)))
  * The rounding of deriv is taken at deriv -/+ err_scale * (fp32 error bound of
  * deriv); the two chains bound any fp32 evaluation (err_scale 0: exact chain). */
-static int rms_bwd_x_impl(int dt, int n_rows, int n_cols, const float * ws, const float * rs, const void * W, const void * X,
+static int rms_bwd_x_impl(int fdt, int dt, int n_rows, int n_cols, const float * ws, const float * rs, const void * W, const void * X,
 							const void * dY, const void * dX_in, double * v_lo, double * v_hi, double err_scale) {
-	if (!dt_ok(dt) || n_rows < 0 || n_cols <= 0) return -1;
+	if (!dt_ok(fdt) || !bwd_dt_ok(dt) || n_rows < 0 || n_cols <= 0) return -1;
 	#pragma omp parallel for schedule(static)
 	for (int r = 0; r < n_rows; r++) {
 		const long base = (long) r * n_cols;
 		const double rr = rs[r], w_s = ws[r];
 		const double r3 = rr * rr * rr;
 		for (int j = 0; j < n_cols; j++) {
-			const double w = load1(dt, W, j), x = load1(dt, X, base + j);
+			const double w = load1(fdt, W, j), x = load1(fdt, X, base + j);
 			const double a = w * rr, b = ((x * r3) / (double) n_cols) * w_s;
 			const double deriv = a - b;
 			const double err = err_scale * 8.0 * U32 * (fabs(a) + fabs(b));
@@ -191,20 +262,26 @@ static int rms_bwd_x_impl(int dt, int n_rows, int n_cols, const float * ws, cons
 
 int oracle_rms_norm_bwd_x(int dt, int n_rows, int n_cols, const float * ws, const float * rs,
 						const void * W, const void * X, const void * dY, const void * dX_in, double * v_lo, double * v_hi) {
-	return rms_bwd_x_impl(dt, n_rows, n_cols, ws, rs, W, X, dY, dX_in, v_lo, v_hi, 1.0);
+	return rms_bwd_x_impl(dt, dt, n_rows, n_cols, ws, rs, W, X, dY, dX_in, v_lo, v_hi, 1.0);
+}
+
+/* W and X in fdt (fp8 allowed), dY and dX in dt */
+int oracle_rms_norm_bwd_x2(int fdt, int dt, int n_rows, int n_cols, const float * ws, const float * rs,
+						const void * W, const void * X, const void * dY, const void * dX_in, double * v_lo, double * v_hi) {
+	return rms_bwd_x_impl(fdt, dt, n_rows, n_cols, ws, rs, W, X, dY, dX_in, v_lo, v_hi, 1.0);
 }
 
 /* reference: src/ops/nvidia/norm/rms_norm_bwd_w.cu:211-308 (bf16), :4-101 (fp32):
  * dW += sum_rows dY * x * rstd, summed here in fp64 (the reference's bf16
  * atomics have no defined order) */
-static void dw_accumulate(int dt, int n_rows, int n_cols, const float * rs, const void * X, const void * dY,
+static void dw_accumulate(int fdt, int dt, int n_rows, int n_cols, const float * rs, const void * X, const void * dY,
 							double * dw_pre, double * dw_abs) {
 	#pragma omp parallel for schedule(static)
 	for (int j = 0; j < n_cols; j++) {
 		double s = 0.0, a = 0.0;
 		for (int r = 0; r < n_rows; r++) {
 			const long i = (long) r * n_cols + j;
-			const double t = load1(dt, dY, i) * load1(dt, X, i) * (double) rs[r];
+			const double t = load1(dt, dY, i) * load1(fdt, X, i) * (double) rs[r];
 			s += t;
 			a += fabs(t);
 		}
@@ -215,12 +292,18 @@ static void dw_accumulate(int dt, int n_rows, int n_cols, const float * rs, cons
 
 int oracle_rms_norm_bwd_w(int dt, int dt_w, int n_rows, int n_cols, const float * rs, const void * X, const void * dY,
 						const void * dW_in, double * dw_pre, double * dw_abs) {
-	if (!dt_ok(dt) || !dt_ok(dt_w) || n_rows < 0 || n_cols <= 0) return -1;
+	return oracle_rms_norm_bwd_w2(dt, dt, dt_w, n_rows, n_cols, rs, X, dY, dW_in, dw_pre, dw_abs);
+}
+
+/* X in fdt (fp8 allowed), dY in dt, dW in dt_w (rms_norm_bwd_w.cu:310-700 for fp8 X) */
+int oracle_rms_norm_bwd_w2(int fdt, int dt, int dt_w, int n_rows, int n_cols, const float * rs, const void * X, const void * dY,
+						const void * dW_in, double * dw_pre, double * dw_abs) {
+	if (!dt_ok(fdt) || !bwd_dt_ok(dt) || !bwd_dt_ok(dt_w) || n_rows < 0 || n_cols <= 0) return -1;
 	for (int j = 0; j < n_cols; j++) {
 		dw_pre[j] = load1(dt_w, dW_in, j);
 		if (dw_abs) dw_abs[j] = fabs(dw_pre[j]);
 	}
-	dw_accumulate(dt, n_rows, n_cols, rs, X, dY, dw_pre, dw_abs);
+	dw_accumulate(fdt, dt, n_rows, n_cols, rs, X, dY, dw_pre, dw_abs);
 	return 0;
 }
 
@@ -229,7 +312,7 @@ int oracle_rms_norm_bwd_w(int dt, int dt_w, int n_rows, int n_cols, const float 
  *   dX += r*(dY*w) - x * r^3/n * sum_j(dY*w*x);  dW += sum_rows dY*x*r */
 int oracle_rms_norm_bwd(int dt, int n_rows, int n_cols, const float * rs, const void * W, const void * X, const void * dY,
 						const void * dX_in, const float * dW_in, double * dx_pre, double * dx_floor, double * dw_pre, double * dw_abs) {
-	if (!dt_ok(dt) || n_rows < 0 || n_cols <= 0) return -1;
+	if (!bwd_dt_ok(dt) || n_rows < 0 || n_cols <= 0) return -1;
 	#pragma omp parallel for schedule(static)
 	for (int r = 0; r < n_rows; r++) {
 		const long base = (long) r * n_cols;
@@ -254,7 +337,7 @@ int oracle_rms_norm_bwd(int dt, int n_rows, int n_cols, const float * rs, const 
 		dw_pre[j] = (double) dW_in[j];
 		if (dw_abs) dw_abs[j] = fabs(dw_pre[j]);
 	}
-	dw_accumulate(dt, n_rows, n_cols, rs, X, dY, dw_pre, dw_abs);
+	dw_accumulate(dt, dt, n_rows, n_cols, rs, X, dY, dw_pre, dw_abs);
 	return 0;
 }
 
@@ -333,10 +416,15 @@ int oracle_swiglu(int dt, long n, const void * g, const void * u, double * out_p
  * evaluated in its sigmoid form. dg_floor bounds the fp32 evaluation noise of
  * dG, whose factor (1 + g*(1-sigmoid(g))) crosses zero near g = -1.28. */
 int oracle_swiglu_bwd(int dt, long n, const void * g, const void * u, const void * dO, double * dg_pre, double * dg_floor, double * du_pre) {
-	if (!dt_ok(dt) || n < 0) return -1;
+	return oracle_swiglu_bwd2(dt, dt, n, g, u, dO, dg_pre, dg_floor, du_pre);
+}
+
+/* g and u in fdt (fp8 allowed: swiglu_bwd_x.cu:82-187), dO in dt */
+int oracle_swiglu_bwd2(int fdt, int dt, long n, const void * g, const void * u, const void * dO, double * dg_pre, double * dg_floor, double * du_pre) {
+	if (!dt_ok(fdt) || !bwd_dt_ok(dt) || n < 0) return -1;
 	#pragma omp parallel for schedule(static)
 	for (long i = 0; i < n; i++) {
-		const double gv = load1(dt, g, i), uv = load1(dt, u, i), d = load1(dt, dO, i);
+		const double gv = load1(fdt, g, i), uv = load1(fdt, u, i), d = load1(dt, dO, i);
 		const double e = exp(-gv);
 		double sig, dg;
 		if (isfinite(e)) {
@@ -356,10 +444,13 @@ int oracle_swiglu_bwd(int dt, long n, const void * g, const void * u, const void
 
 /* ---------------- softmax / cross-entropy ---------------- */
 
-/* reference: src/ops/nvidia/loss/softmax.cu:273-407 (bf16), :3-140 (fp32):
- *   m = max x;  d = rnd_in((float) x - (float) m);  y = exp(d) / sum exp(d)
- * (the fp32 kernel uses the fp32 difference itself) */
-static void softmax_row(int dt_in, const void * X, long base, int n_cols, double * y, double * m_out, double * sx_out) {
+/* reference: src/ops/nvidia/loss/softmax.cu:273-407 (bf16), :3-140 (fp32),
+ * :409-960 (fp8 inputs, fp16 / bf16 outputs):
+ *   m = max x;  d = rnd((float) x - (float) m);  y = exp(d) / sum exp(d)
+ * with rnd the rounding to the input type (the fp32 kernel uses the fp32
+ * difference itself); fp8 inputs are converted to the output type first and
+ * subtracted there, so `dt_diff` is the output type for them */
+static void softmax_row(int dt_in, int dt_diff, const void * X, long base, int n_cols, double * y, double * m_out, double * sx_out) {
 	double m = -INFINITY;
 	for (int j = 0; j < n_cols; j++) {
 		const double x = load1(dt_in, X, base + j);
@@ -369,7 +460,7 @@ static void softmax_row(int dt_in, const void * X, long base, int n_cols, double
 	for (int j = 0; j < n_cols; j++) {
 		const float x = (float) load1(dt_in, X, base + j);
 		const float diff = x - (float) m;
-		const double d = oracle_round((double) diff, dt_in);
+		const double d = oracle_round((double) diff, dt_diff);
 		const double e = exp(d);
 		y[base + j] = e;
 		s += e;
@@ -381,9 +472,10 @@ static void softmax_row(int dt_in, const void * X, long base, int n_cols, double
 }
 
 int oracle_softmax(int dt_in, int dt_out, int n_rows, int n_cols, const void * X, double * y_pre) {
-	if (!dt_ok(dt_in) || !dt_ok(dt_out) || n_rows < 0 || n_cols <= 0) return -1;
+	if (!dt_ok(dt_in) || !bwd_dt_ok(dt_out) || n_rows < 0 || n_cols <= 0) return -1;
+	const int dt_diff = is_fp8(dt_in) ? dt_out : dt_in;
 	#pragma omp parallel for schedule(static)
-	for (int r = 0; r < n_rows; r++) softmax_row(dt_in, X, (long) r * n_cols, n_cols, y_pre, NULL, NULL);
+	for (int r = 0; r < n_rows; r++) softmax_row(dt_in, dt_diff, X, (long) r * n_cols, n_cols, y_pre, NULL, NULL);
 	return 0;
 }
 
@@ -391,7 +483,7 @@ int oracle_softmax(int dt_in, int dt_out, int n_rows, int n_cols, const void * X
  * (the kernel's row index i / n_cols is always 0, so it only ever touches
  * row 0): P[r, label_r] = rnd((float) P - 1) in place; labels >= n_cols skip. */
 int oracle_cross_entropy_loss(int dt, int n_rows, int n_cols, void * P, const uint32_t * labels) {
-	if (!dt_ok(dt) || n_rows < 0 || n_cols <= 0) return -1;
+	if (!bwd_dt_ok(dt) || n_rows < 0 || n_cols <= 0) return -1;
 	for (int r = 0; r < n_rows; r++) {
 		if (labels[r] >= (uint32_t) n_cols) continue;
 		const long i = (long) r * n_cols + labels[r];
@@ -409,12 +501,12 @@ int oracle_cross_entropy_loss(int dt, int n_rows, int n_cols, void * P, const ui
  * y (1 -/+ 1e-5) to cover the fp32 error of any evaluation of y. */
 static int softmax_xent_impl(int dt, int n_rows, int n_cols, const void * X, const uint32_t * labels,
 								double * y_lo, double * y_hi, double * loss, double * mean_loss, double slack) {
-	if (!dt_ok(dt) || n_rows < 0 || n_cols <= 0) return -1;
+	if (!bwd_dt_ok(dt) || n_rows < 0 || n_cols <= 0) return -1;
 	#pragma omp parallel for schedule(static)
 	for (int r = 0; r < n_rows; r++) {
 		const long base = (long) r * n_cols;
 		double m, sx;
-		softmax_row(dt, X, base, n_cols, y_lo, &m, &sx);
+		softmax_row(dt, dt, X, base, n_cols, y_lo, &m, &sx);
 		if (y_hi) memcpy(y_hi + base, y_lo + base, sizeof(double) * (size_t) n_cols);
 		const uint32_t lab = labels[r];
 		if (lab < (uint32_t) n_cols) {
@@ -445,7 +537,12 @@ int oracle_softmax_cross_entropy(int dt, int n_rows, int n_cols, const void * X,
 /* exact chains (no evaluation slack), for the CPU dispatch adapters */
 int oracle_rms_norm_bwd_x_exact(int dt, int n_rows, int n_cols, const float * ws, const float * rs,
 						const void * W, const void * X, const void * dY, const void * dX_in, double * v) {
-	return rms_bwd_x_impl(dt, n_rows, n_cols, ws, rs, W, X, dY, dX_in, v, NULL, 0.0);
+	return rms_bwd_x_impl(dt, dt, n_rows, n_cols, ws, rs, W, X, dY, dX_in, v, NULL, 0.0);
+}
+
+int oracle_rms_norm_bwd_x2_exact(int fdt, int dt, int n_rows, int n_cols, const float * ws, const float * rs,
+						const void * W, const void * X, const void * dY, const void * dX_in, double * v) {
+	return rms_bwd_x_impl(fdt, dt, n_rows, n_cols, ws, rs, W, X, dY, dX_in, v, NULL, 0.0);
 }
 
 int oracle_softmax_cross_entropy_exact(int dt, int n_rows, int n_cols, const void * X, const uint32_t * labels,

@@ -6,7 +6,10 @@
  * cpu_baseline leg may load it, and only as the checker or the reported CPU
  * baseline; the product library never links or calls it.
  *
- * dtype codes are DataflowDatatype values: FP32 = 3, FP16 = 4, BF16 = 5.
+ * dtype codes are DataflowDatatype values: FP32 = 3, FP16 = 4, BF16 = 5,
+ * FP8E4M3 = 6, FP8E5M2 = 7 (OCP 8-bit formats; forward-type tensors only:
+ * the "2" variants take the forward tensors' type and the backward ones'
+ * separately, as the reference's fp8 x {fp16, bf16} kernels do).
  * Outputs named *_pre are the exact value before the final rounding to the
  * output type ("v" of the parity criterion |o - v| <= ulp(v)). Where the
  * reference rounds intermediates, the oracle returns [lo, hi] bounds of that
@@ -25,6 +28,8 @@
 #define ORACLE_FP32 3
 #define ORACLE_FP16 4
 #define ORACLE_BF16 5
+#define ORACLE_FP8E4M3 6
+#define ORACLE_FP8E5M2 7
 
 double oracle_round(double v, int dt);
 double oracle_ulp(double v, int dt);
@@ -38,12 +43,18 @@ int oracle_rms_norm_bwd_x(int dt, int n_rows, int n_cols, const float * ws, cons
 					const void * W, const void * X, const void * dY, const void * dX_in, double * v_lo, double * v_hi);
 int oracle_rms_norm_bwd_w(int dt, int dt_w, int n_rows, int n_cols, const float * rs, const void * X, const void * dY,
 					const void * dW_in, double * dw_pre, double * dw_abs);
+int oracle_rms_norm_sq_sums(int dt, int n_rows, int n_cols, const void * X, double * sq_sums);
+int oracle_rms_norm_bwd_x2(int fdt, int dt, int n_rows, int n_cols, const float * ws, const float * rs,
+					const void * W, const void * X, const void * dY, const void * dX_in, double * v_lo, double * v_hi);
+int oracle_rms_norm_bwd_w2(int fdt, int dt, int dt_w, int n_rows, int n_cols, const float * rs, const void * X, const void * dY,
+					const void * dW_in, double * dw_pre, double * dw_abs);
 int oracle_rms_norm_bwd(int dt, int n_rows, int n_cols, const float * rs, const void * W, const void * X, const void * dY,
 					const void * dX_in, const float * dW_in, double * dx_pre, double * dx_floor, double * dw_pre, double * dw_abs);
 int oracle_rope(int dt, int bwd, uint64_t N, int model_dim, int head_dim, int num_kv_heads, int theta, const int * seq_positions,
 					const void * X_q, const void * X_k, double * q_pre, double * k_pre);
 int oracle_swiglu(int dt, long n, const void * g, const void * u, double * out_pre);
 int oracle_swiglu_bwd(int dt, long n, const void * g, const void * u, const void * dO, double * dg_pre, double * dg_floor, double * du_pre);
+int oracle_swiglu_bwd2(int fdt, int dt, long n, const void * g, const void * u, const void * dO, double * dg_pre, double * dg_floor, double * du_pre);
 int oracle_softmax(int dt_in, int dt_out, int n_rows, int n_cols, const void * X, double * y_pre);
 int oracle_cross_entropy_loss(int dt, int n_rows, int n_cols, void * P, const uint32_t * labels);
 int oracle_softmax_cross_entropy(int dt, int n_rows, int n_cols, const void * X, const uint32_t * labels,
@@ -63,5 +74,7 @@ int oracle_rms_norm_bwd_x_exact(int dt, int n_rows, int n_cols, const float * ws
 					const void * W, const void * X, const void * dY, const void * dX_in, double * v);
 int oracle_softmax_cross_entropy_exact(int dt, int n_rows, int n_cols, const void * X, const uint32_t * labels,
 					double * y, double * loss, double * mean_loss);
+int oracle_rms_norm_bwd_x2_exact(int fdt, int dt, int n_rows, int n_cols, const float * ws, const float * rs,
+					const void * W, const void * X, const void * dY, const void * dX_in, double * v);
 
 #endif

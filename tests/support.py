@@ -13,8 +13,11 @@ ORACLE_LIB = os.path.join(ROOT, "oracle", "liboracle.so")
 REF_HOST_LIB = os.path.join(ROOT, "oracle", "_ref", "libref_host.so")
 
 FP32, FP16, BF16 = 3, 4, 5
-NP_STORAGE = {FP32: np.float32, FP16: np.float16, BF16: np.uint16}
-FORMAT = {FP32: (24, -126), FP16: (11, -14), BF16: (8, -126)}   # (mantissa bits incl. implicit, emin)
+FP8E4M3, FP8E5M2 = 6, 7   # OCP 8-bit formats, stored as uint8 codes
+NP_STORAGE = {FP32: np.float32, FP16: np.float16, BF16: np.uint16, FP8E4M3: np.uint8, FP8E5M2: np.uint8}
+# (mantissa bits incl. implicit, emin)
+FORMAT = {FP32: (24, -126), FP16: (11, -14), BF16: (8, -126), FP8E4M3: (4, -6), FP8E5M2: (3, -14)}
+FP8_MAX = {FP8E4M3: 448.0, FP8E5M2: 57344.0}
 
 _oracle = None
 
@@ -42,6 +45,10 @@ def oracle():
         L.oracle_softmax_cross_entropy.argtypes = [i, i, i, vp, vp, vp, vp, vp, vp]
         L.oracle_embedding.argtypes = [i, i, i, vp, vp, ctypes.c_long, vp]
         L.oracle_copy_to_seq_context.argtypes = [i, ctypes.c_uint64, i, vp, vp, vp, vp, vp]
+        L.oracle_rms_norm_bwd_x2.argtypes = [i, i, i, i, vp, vp, vp, vp, vp, vp, vp, vp]
+        L.oracle_rms_norm_bwd_w2.argtypes = [i, i, i, i, i, vp, vp, vp, vp, vp, vp]
+        L.oracle_rms_norm_sq_sums.argtypes = [i, i, i, vp, vp]
+        L.oracle_swiglu_bwd2.argtypes = [i, i, ctypes.c_long, vp, vp, vp, vp, vp, vp]
         L.oracle_load.argtypes = [i, vp, ctypes.c_long, vp]
         L.oracle_store.argtypes = [i, vp, ctypes.c_long, vp]
         _oracle = L
@@ -70,8 +77,13 @@ def bf16_bits_to_f32(b):
 
 
 def to_storage(x32, dt):
-    """fp32 values -> storage array of dtype dt (RNE)."""
+    """fp32 values -> storage array of dtype dt (RNE; fp8 saturates to +-max)."""
     x32 = np.asarray(x32, dtype=np.float32)
+    if dt in FP8_MAX:
+        v = np.ascontiguousarray(x32, dtype=np.float64)
+        out = np.empty(v.shape, np.uint8)
+        oracle().oracle_store(dt, ptr(v), v.size, ptr(out))
+        return out
     if dt == FP32:
         return x32.copy()
     if dt == FP16:
@@ -80,6 +92,11 @@ def to_storage(x32, dt):
 
 
 def to_f64(a, dt):
+    if dt in FP8_MAX:
+        a = np.ascontiguousarray(a, dtype=np.uint8)
+        out = np.empty(a.shape)
+        oracle().oracle_load(dt, ptr(a), a.size, ptr(out))
+        return out
     if dt == BF16:
         return bf16_bits_to_f32(a).astype(np.float64)
     return np.asarray(a).astype(np.float64)
@@ -111,10 +128,13 @@ def check_rounded(o, dt, v_lo, v_hi=None, floor=None, what=""):
     of the exact pre-rounding value, or of the [v_lo, v_hi] interval when the
     reference rounds an intermediate. `floor` adds an fp32-evaluation noise
     bound where the exact expression cancels. Values in the fp32 subnormal
-    range may flush to zero. fp32 outputs use 1e-5 relative instead of 1 ulp."""
+    range may flush to zero. fp32 outputs use 1e-5 relative instead of 1 ulp.
+    fp8 outputs saturate: the expected values are clamped to +-max first."""
     of = to_f64(o, dt).ravel()
     lo = np.asarray(v_lo, dtype=np.float64).ravel()
     hi = lo if v_hi is None else np.asarray(v_hi, dtype=np.float64).ravel()
+    if dt in FP8_MAX:
+        lo, hi = np.clip(lo, -FP8_MAX[dt], FP8_MAX[dt]), np.clip(hi, -FP8_MAX[dt], FP8_MAX[dt])
     a, b = np.minimum(lo, hi), np.maximum(lo, hi)
     fl = 0.0 if floor is None else np.asarray(floor, dtype=np.float64).ravel()
     if dt == FP32:
@@ -160,7 +180,7 @@ RMS_CH, RMS_MAX_TPR, RMS_STREAM_TPR = 2, 1024, 256
 RMS_CELLS_PER_SLOT, RMS_INFLIGHT_BYTES = 64, 64 * 1024
 RMS_STREAM_WIDE_COLS, RMS_FIN_GROUPS = 4096, 256 // 16   # finish: RMS_FINISH_THREADS / RMS_FIN_COLS
 RMS_DW_SCRATCH_FLOATS = 4 << 20
-ELEM_BYTES = {FP32: 4, FP16: 2, BF16: 2}
+ELEM_BYTES = {FP32: 4, FP16: 2, BF16: 2, FP8E4M3: 1, FP8E5M2: 1}
 
 
 def gamma(d):
@@ -223,3 +243,13 @@ def rms_dw_depth(dt, n_rows, n_cols, arrays, cu_count, max_lds, aligned=True):
     rows = -(-n_rows // (grid * slots))
     finish = -(-grid // RMS_FIN_GROUPS) + RMS_FIN_GROUPS + 1
     return rows + (slots - 1) + finish + (1 if dt == FP32 else 0)
+
+
+def rms_dw_fp8_depth(n_rows, n_cols, cu_count):
+    """roundings along the dW reduction of the fp8-input rms_norm_bwd_w
+    (fp8_ops.hip, launch shape in hip_ops_config.c): a workgroup's rows in
+    sequence into its LDS row (fp8 x 16-bit products are exact in fp32), then
+    the same finish pass as the other types"""
+    grid = min(n_rows, cu_count, RMS_DW_SCRATCH_FLOATS // n_cols)
+    rows = -(-n_rows // grid)
+    return rows + (-(-grid // RMS_FIN_GROUPS) + RMS_FIN_GROUPS + 1)

@@ -28,7 +28,7 @@ def build_and_run(tmp_path):
 def test_c_caller_config1_and_layouts(tmp_path):
     r = build_and_run(tmp_path)
     assert r.returncode == 0, r.stdout + r.stderr
-    assert "OK registered 46" in r.stdout
+    assert "OK registered 68" in r.stdout
     layout = {}
     for line in r.stdout.splitlines():
         if line.startswith("LAYOUT "):

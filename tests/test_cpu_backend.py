@@ -28,8 +28,9 @@ def cpu_handle():
 
 def test_registers_every_variant(cpu_handle):
     h, n = cpu_handle
-    # 12 arithmetic ops x fp32/fp16/bf16, plus embedding and copy_to_seq_context x 5 storage types
-    assert n == 46 and h.num_ops == 46 and h.op_table.cnt == 46
+    # the reference's 54 functions (its fp8 variants included), copy_to_seq_context x 5 storage
+    # types and the three fused ops x fp32/fp16/bf16
+    assert n == 68 and h.num_ops == 68 and h.op_table.cnt == 68
 
 
 def test_config1_rms_norm_fp32_through_handle(cpu_handle):
@@ -66,8 +67,8 @@ def test_dispatch_uses_fingerprint_not_name(cpu_handle):
 def test_error_paths(cpu_handle):
     h, _ = cpu_handle
     p = np.zeros(64, np.float32)
-    # unknown variant (fp8 is not provided) and an out-of-range stream id
-    assert api.submit_rms_norm(ctypes.byref(h), 0, api.DATAFLOW_FP8E4M3, 1, 16, 1e-5, ptr(p), ptr(p), ptr(p), None, None) == -1
+    # a variant nobody registers (uint8 storage) and an out-of-range stream id
+    assert api.submit_rms_norm(ctypes.byref(h), 0, api.DATAFLOW_UINT8, 1, 16, 1e-5, ptr(p), ptr(p), ptr(p), None, None) == -1
     assert api.submit_rms_norm(ctypes.byref(h), 5, FP32, 1, 16, 1e-5, ptr(p), ptr(p), ptr(p), None, None) == -1
     assert api.submit_rms_norm(ctypes.byref(h), -1, FP32, 1, 16, 1e-5, ptr(p), ptr(p), ptr(p), None, None) == 0
 

@@ -63,6 +63,14 @@ def test_kernel_code_object_present():
                 b"swiglu_bwd_x_bf16_bf16_kernel", b"softmax_cross_entropy_loss_bf16_kernel", b"embedding_fp8e5m2_kernel",
                 b"copy_to_seq_context_bf16_kernel", b"rope_copy_to_seq_context_bf16_kernel"):
         assert sym in data
+    # the 22 functions with fp8 tensors: every kernel name the registry derives for them
+    for f in ("fp8e4m3", "fp8e5m2"):
+        for name in ("rms_norm_%s_kernel", "rope_%s_kernel", "swiglu_%s_kernel"):
+            assert (name % f).encode() in data
+        for b in ("fp16", "bf16"):
+            for op in ("rms_norm_bwd_x", "rms_norm_bwd_w", "swiglu_bwd_x", "softmax"):
+                assert ("%s_%s_%s_kernel" % (op, f, b)).encode() in data
+            assert ("rms_norm_bwd_w_%s_%s_kernel_finish" % (f, b)).encode() in data
     # the measurement-only streaming copies live in bench.py's own code object
     assert b"dataflow_stream_copy" not in data
     bench = open(api.BENCH_COPY_KERNELS, "rb").read()

@@ -712,8 +712,8 @@ def test_unknown_variant_and_bad_stream(hdl):
     from dataflow_lib_amd import api
     with Dev(hdl) as d:
         p = d.empty(1024)
-        # fp8 RMSNorm is a reference variant this library does not provide
-        assert api.submit_rms_norm(hdl, 0, api.DATAFLOW_FP8E4M3, 1, 16, 1e-5, p, p, p, None, None) == -1
+        # uint8 storage: no op registers it
+        assert api.submit_rms_norm(hdl, 0, api.DATAFLOW_UINT8, 1, 16, 1e-5, p, p, p, None, None) == -1
         assert api.submit_swiglu(hdl, 7, BF16, 1, 8, p, p, p) == -1
 
 

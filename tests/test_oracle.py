@@ -402,3 +402,104 @@ def test_copy_to_seq_context_places_keys_then_values():
             if r not in tset:
                 assert np.all(c[r] == -7.0)
     assert O.oracle_copy_to_seq_context(4, n_tok * kv_dim + 1, kv_dim, ptr(K), ptr(V), ptr(pos), ptr(ptrs), ptr(sizes)) == -1
+
+
+# ---------------- fp8 (OCP E4M3 / E5M2) ----------------
+
+FP8E4M3, FP8E5M2 = 6, 7
+FP8_MAX = {FP8E4M3: 448.0, FP8E5M2: 57344.0}
+
+
+def fp8_decode_all(dt):
+    codes = np.arange(256, dtype=np.uint8)
+    out = np.empty(256)
+    O.oracle_load(dt, ptr(codes), 256, ptr(out))
+    return out
+
+
+def fp8_encode(dt, vals):
+    v = np.ascontiguousarray(vals, dtype=np.float64)
+    out = np.empty(v.size, np.uint8)
+    O.oracle_store(dt, ptr(v), v.size, ptr(out))
+    return out
+
+
+def test_fp8_decode_every_code():
+    import torch
+    codes = np.arange(256, dtype=np.uint8)
+    # E5M2 is the upper byte of IEEE binary16, so numpy's fp16 decodes it independently
+    e5 = fp8_decode_all(FP8E5M2)
+    ref5 = (codes.astype(np.uint16) << 8).view(np.float16).astype(np.float64)
+    assert np.array_equal(np.isnan(e5), np.isnan(ref5)) and np.array_equal(e5[~np.isnan(e5)], ref5[~np.isnan(ref5)])
+    for dt, tdt in ((FP8E4M3, torch.float8_e4m3fn), (FP8E5M2, torch.float8_e5m2)):
+        got = fp8_decode_all(dt)
+        ref = torch.from_numpy(codes.copy()).view(tdt).to(torch.float64).numpy()
+        assert np.array_equal(np.isnan(got), np.isnan(ref)), dt
+        assert np.array_equal(got[~np.isnan(got)], ref[~np.isnan(ref)]), dt
+    e4 = fp8_decode_all(FP8E4M3)
+    # E4M3: no infinities, one NaN pattern per sign, largest 448, smallest subnormal 2^-9
+    assert np.isnan(e4).sum() == 2 and np.isnan(e4[0x7f]) and np.isnan(e4[0xff])
+    assert np.nanmax(e4) == 448.0 and e4[1] == 2.0 ** -9 and not np.isinf(e4).any()
+    assert np.isinf(e5).sum() == 2 and np.nanmax(e5[np.isfinite(e5)]) == 57344.0 and e5[1] == 2.0 ** -16
+
+
+@pytest.mark.parametrize("dt", [FP8E4M3, FP8E5M2], ids=["e4m3", "e5m2"])
+def test_fp8_encode_rounding_and_saturation(dt):
+    import torch
+    tdt = torch.float8_e4m3fn if dt == FP8E4M3 else torch.float8_e5m2
+    vals = fp8_decode_all(dt)
+    fin = np.sort(np.unique(vals[np.isfinite(vals)]))
+    # every code's value comes back to its code (both zeros keep their sign)
+    codes = np.arange(256, dtype=np.uint8)
+    keep = np.isfinite(vals)
+    assert np.array_equal(fp8_encode(dt, vals[keep]), codes[keep])
+    # midpoints between neighbours go to the even code, values just off a
+    # midpoint to the nearer one; plus random fp32 values across the range
+    mid = (fin[1:] + fin[:-1]) / 2
+    g = rng(7)
+    rand = (g.standard_normal(20000) * 2.0 ** g.integers(-18, 17, 20000)).astype(np.float32).astype(np.float64)
+    probe = np.concatenate([mid, np.nextafter(mid, np.inf), np.nextafter(mid, -np.inf), rand])
+    probe = probe[np.abs(probe) <= FP8_MAX[dt]].astype(np.float32).astype(np.float64)
+    got = fp8_encode(dt, probe)
+    ref = torch.from_numpy(probe.astype(np.float32)).to(tdt).view(torch.uint8).numpy()
+    same = got == ref
+    # +-0 of a value that rounds to zero may differ in sign only
+    zero = (vals[got] == 0) & (vals[ref] == 0)
+    assert np.all(same | zero)
+    # saturating conversion: past the largest finite value (and infinity) to +-max; NaN stays NaN
+    big = np.array([FP8_MAX[dt] * 1.0625, FP8_MAX[dt] * 4, 1e30, np.inf, -FP8_MAX[dt] * 2, -np.inf])
+    dec = vals[fp8_encode(dt, big)]
+    assert np.array_equal(dec, np.sign(big) * FP8_MAX[dt])
+    assert np.isnan(vals[fp8_encode(dt, np.array([np.nan]))[0]])
+    # oracle_round agrees with the code it stores
+    for x in probe[:200]:
+        assert O.oracle_round(x, dt) == vals[fp8_encode(dt, np.array([x]))[0]]
+
+
+def test_fp8_mixed_type_functions_reduce_to_the_single_type_ones():
+    """the *2 variants with equal forward and backward types equal the
+    single-type functions, and an fp8 forward type reads its tensors as fp8"""
+    n_rows, n_cols = 6, 64
+    X, W = to_storage(normal(60, (n_rows, n_cols)), BF16), to_storage(1 + normal(61, (n_cols,), std=0.02), BF16)
+    dY, dX = to_storage(normal(62, (n_rows, n_cols)), BF16), to_storage(normal(63, (n_rows, n_cols)), BF16)
+    ws, rs = normal(64, (n_rows,)), (1 + np.abs(normal(65, (n_rows,)))).astype(np.float32)
+    a_lo, a_hi, b_lo, b_hi = (np.empty((n_rows, n_cols)) for _ in range(4))
+    assert O.oracle_rms_norm_bwd_x(BF16, n_rows, n_cols, ptr(ws), ptr(rs), ptr(W), ptr(X), ptr(dY), ptr(dX), ptr(a_lo), ptr(a_hi)) == 0
+    assert O.oracle_rms_norm_bwd_x2(BF16, BF16, n_rows, n_cols, ptr(ws), ptr(rs), ptr(W), ptr(X), ptr(dY), ptr(dX), ptr(b_lo), ptr(b_hi)) == 0
+    assert np.array_equal(a_lo, b_lo) and np.array_equal(a_hi, b_hi)
+    # fp8 X and W: the same values stored as bf16 give the same result
+    X8 = fp8_encode(FP8E4M3, to_f64(X, BF16).ravel()).reshape(X.shape)
+    W8 = fp8_encode(FP8E4M3, to_f64(W, BF16))
+    X8b = to_storage(fp8_decode_all(FP8E4M3)[X8].astype(np.float32), BF16)
+    W8b = to_storage(fp8_decode_all(FP8E4M3)[W8].astype(np.float32), BF16)
+    c_lo, c_hi, d_lo, d_hi = (np.empty((n_rows, n_cols)) for _ in range(4))
+    assert O.oracle_rms_norm_bwd_x2(FP8E4M3, BF16, n_rows, n_cols, ptr(ws), ptr(rs), ptr(W8), ptr(X8), ptr(dY), ptr(dX), ptr(c_lo), ptr(c_hi)) == 0
+    assert O.oracle_rms_norm_bwd_x2(BF16, BF16, n_rows, n_cols, ptr(ws), ptr(rs), ptr(W8b), ptr(X8b), ptr(dY), ptr(dX), ptr(d_lo), ptr(d_hi)) == 0
+    assert np.array_equal(c_lo, d_lo) and np.array_equal(c_hi, d_hi)
+    # backward-only tensors refuse fp8
+    assert O.oracle_rms_norm_bwd_x2(BF16, FP8E4M3, n_rows, n_cols, ptr(ws), ptr(rs), ptr(W), ptr(X), ptr(dY), ptr(dX), ptr(c_lo), ptr(c_hi)) == -1
+    # sum of squares (the fp8 forward's statistic) against numpy
+    ss = np.empty(n_rows)
+    assert O.oracle_rms_norm_sq_sums(FP8E4M3, n_rows, n_cols, ptr(X8), ptr(ss)) == 0
+    xv = fp8_decode_all(FP8E4M3)[X8]
+    assert np.allclose(ss, (xv * xv).sum(1), rtol=1e-15)
