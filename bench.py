@@ -109,6 +109,21 @@ def bf16_bits(x):
     return ((u + 0x7FFF + ((u >> 16) & 1)) >> 16).astype(np.uint16)
 
 
+def fp8e4m3_bits(x):
+    """fp32 -> OCP E4M3 codes (bias 7, 3 mantissa bits), round to nearest
+    even, saturating at +-448 (synthetic inputs of the fp8 extras)"""
+    x = np.asarray(x, np.float64)
+    sign = np.signbit(x).astype(np.uint8) << 7
+    a = np.minimum(np.abs(x), 448.0)
+    quantum = np.exp2(np.floor(np.log2(np.maximum(a, 2.0 ** -6))) - 3)
+    r = np.round(a / quantum) * quantum
+    e = np.floor(np.log2(np.maximum(r, 2.0 ** -6)))
+    normal = r >= 2.0 ** -6
+    field = np.where(normal, e + 7, 0).astype(np.uint8)
+    mant = (np.where(normal, r / np.exp2(e) - 1.0, r / 2.0 ** -6) * 8).astype(np.uint8)
+    return sign | (field << 3) | mant
+
+
 class Pool:
     """Device buffers filled by tiling seeded host blocks (device-to-device copies)."""
 
@@ -122,6 +137,8 @@ class Pool:
             g = np.random.default_rng(seed)
             if kind == "normal_bf16":
                 host = bf16_bits(a + b * g.standard_normal(self.block_elems, dtype=np.float32))
+            elif kind == "normal_fp8e4m3":
+                host = fp8e4m3_bits(a + b * g.standard_normal(self.block_elems, dtype=np.float32))
             elif kind == "zeros":
                 host = np.zeros(self.block_elems, np.uint16)
             else:
@@ -297,6 +314,53 @@ def build_extras(h, pool, api):
         runs.append(lambda Q=Q, K=K, Vv=Vv, pp=pp, ptrs=ptrs, ps=ps:
                     api.submit_rope_copy_to_seq_context(h, 0, BF16, T * 4096, 4096, 128, 8, 500000, pp, Q, K, Vv, ptrs, ps))
     ops.append(("rope_copy_to_seq_context", 2 * q + 5 * kv + T * (4 + 8 + 4), runs))
+    ops += build_fp8_extras(h, pool, api)
+    return ops
+
+
+def build_fp8_extras(h, pool, api):
+    """The fp8 variants at the step's shapes, E4M3 forward tensors and bf16
+    backward ones (E5M2 runs the same kernels with another decode)."""
+    E4, ops = api.DATAFLOW_FP8E4M3, []
+    T, D, F, R, V = 8192, 4096, 14336, 4096, 128256
+    a8, a16 = T * D, T * D * 2
+    runs_f, runs_x, runs_w = [], [], []
+    for s in range(n_sets(2 * a8 + 3 * a16)):
+        X = pool.fill(a8, "normal_fp8e4m3", 50)
+        W = pool.fill(D, "normal_fp8e4m3", 51, 1.0, 0.02)
+        Y, ws, ss = pool.empty(a8), pool.empty(T * 4), pool.empty(T * 4)
+        dY, dX, dW = pool.fill(a16, "normal_bf16", 52), pool.fill(a16, "zeros"), pool.fill(D * 2, "zeros")
+        rs = pool.fill(T * 4, "zeros")
+        runs_f.append(lambda X=X, W=W, Y=Y, ws=ws, ss=ss: api.submit_rms_norm(h, 0, E4, T, D, 1e-5, W, X, Y, ws, ss))
+        runs_x.append(lambda X=X, W=W, dY=dY, dX=dX, ws=ws, rs=rs:
+                      api.submit_rms_norm_bwd_x(h, 0, E4, BF16, T, D, 1e-5, ws, rs, W, X, dY, dX))
+        runs_w.append(lambda X=X, dY=dY, rs=rs, dW=dW: api.submit_rms_norm_bwd_w(h, 0, E4, BF16, T, D, 1e-5, rs, X, dY, dW))
+    ops.append(("rms_norm_fp8e4m3", 2 * a8 + D + T * 4, runs_f))
+    ops.append(("rms_norm_bwd_x_fp8e4m3_bf16", a8 + 3 * a16 + D + 2 * T * 4, runs_x))
+    ops.append(("rms_norm_bwd_w_fp8e4m3_bf16", a8 + a16 + T * 4 + 2 * D * 2, runs_w))
+    q8, k8 = T * 4096, T * 1024
+    pos = np.random.default_rng(53).integers(0, 8192, size=T).astype(np.int32)
+    runs = []
+    for s in range(n_sets(2 * (q8 + k8))):
+        Q, K, pp = pool.fill(q8, "normal_fp8e4m3", 54), pool.fill(k8, "normal_fp8e4m3", 55), pool.put(pos)
+        runs.append(lambda Q=Q, K=K, pp=pp: api.submit_rope(h, 0, E4, T * 4096, 4096, 128, 8, 500000, pp, Q, K))
+    ops.append(("rope_fp8e4m3", 2 * (q8 + k8) + T * 4, runs))
+    f8 = T * F
+    runs_f, runs_b = [], []
+    for s in range(n_sets(3 * f8 + 6 * f8)):
+        G, U = pool.fill(f8, "normal_fp8e4m3", 56, 0.0, 2.0), pool.fill(f8, "normal_fp8e4m3", 57)
+        O, dO = pool.empty(f8), pool.fill(2 * f8, "normal_bf16", 58)
+        dG, dU = pool.empty(2 * f8), pool.empty(2 * f8)
+        runs_f.append(lambda G=G, U=U, O=O: api.submit_swiglu(h, 0, E4, T, F, G, U, O))
+        runs_b.append(lambda G=G, U=U, dO=dO, dG=dG, dU=dU: api.submit_swiglu_bwd_x(h, 0, E4, BF16, T, F, G, U, dO, dG, dU))
+    ops.append(("swiglu_fp8e4m3", 3 * f8, runs_f))
+    ops.append(("swiglu_bwd_x_fp8e4m3_bf16", 8 * f8, runs_b))
+    lg8 = R * V
+    runs = []
+    for s in range(n_sets(3 * lg8)):
+        L, O = pool.fill(lg8, "normal_fp8e4m3", 59, 0.0, 2.0), pool.empty(2 * lg8)
+        runs.append(lambda L=L, O=O: api.submit_softmax(h, 0, E4, BF16, R, V, L, O))
+    ops.append(("softmax_fp8e4m3_bf16", 3 * lg8, runs))
     return ops
 
 

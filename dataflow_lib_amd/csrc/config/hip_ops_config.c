@@ -114,7 +114,17 @@ int rms_norm_bwd_x_set_launch_config(Hip_Launch_Config * hip_launch_config, Data
 	const size_t elem = arg_elem_bytes(hip_function, 5);
 	if (rms_check("rms norm bwd x", n_rows, n_cols, elem)) return -1;
 	if (is_fp8(hip_function, 5)) {
-		rms_fp8_rowwise(hip_launch_config, dataflow_handle, n_rows, n_cols);
+		const int tpr = f8_row_tpr(n_cols);
+		const int vec = tpr > 0 && ((ptr_bits(ARG(op, 5, void *)) | ptr_bits(ARG(op, 6, void *))) & 7ull) == 0 &&
+						((ptr_bits(ARG(op, 7, void *)) | ptr_bits(ARG(op, 8, void *))) & 15ull) == 0;
+		if (!vec) {
+			rms_fp8_rowwise(hip_launch_config, dataflow_handle, n_rows, n_cols);
+			return 0;
+		}
+		/* row slots of tpr threads, 256-thread workgroups */
+		const int slots = MY_MAX(1, 256 / tpr);
+		const long grid = MY_MIN((long) MY_CEIL(n_rows, slots), (long) dev(dataflow_handle)->cu_count * F8_BWDX_WG_PER_CU);
+		set_1d(hip_launch_config, (unsigned) grid, (unsigned) (slots * tpr), 0);
 		return 0;
 	}
 	const int nv = rms_vec_chunks(n_cols, (int) elem, ptr_bits(ARG(op, 5, void *)) | ptr_bits(ARG(op, 6, void *)) |
@@ -160,8 +170,8 @@ int rms_norm_bwd_w_set_launch_config(Hip_Launch_Config * hip_launch_config, Data
 	const size_t elem = arg_elem_bytes(hip_function, 4);
 	if (rms_check("rms norm bwd w", n_rows, n_cols, elem)) return -1;
 	if (is_fp8(hip_function, 4)) {
-		/* fp8 X: one 256-thread workgroup per CU, each summing its rows into an
-		 * LDS row of n_cols floats, one partial row per workgroup */
+		/* fp8 X: one workgroup per CU, each adding its rows into one partial
+		 * row of n_cols floats (combined in LDS) */
 		if (n_rows == 0 || n_cols == 0) {
 			set_1d(hip_launch_config, 0, 1, 0);
 			return 0;
@@ -173,9 +183,15 @@ int rms_norm_bwd_w_set_launch_config(Hip_Launch_Config * hip_launch_config, Data
 			fprintf(stderr, "Error: rms norm bwd w: rows of %d columns need more LDS than the %ld bytes available...\n", n_cols, max_lds);
 			return -1;
 		}
-		long grid = MY_MIN((long) n_rows, (long) dev(dataflow_handle)->cu_count);
+		/* aligned rows of up to 8 * F8_CPT * 1024 columns: row slots of tpr
+		 * threads, as many as fill 1024 threads; otherwise 256 threads
+		 * walking each row */
+		const int tpr = f8_row_tpr(n_cols);
+		const int vec = tpr > 0 && (ptr_bits(ARG(op, 4, void *)) & 7ull) == 0 && (ptr_bits(ARG(op, 5, void *)) & 15ull) == 0;
+		const int slots = vec ? MY_MAX(1, 1024 / tpr) : 1;
+		long grid = MY_MIN((long) MY_CEIL(n_rows, slots), (long) dev(dataflow_handle)->cu_count);
 		grid = MY_MIN(grid, (long) RMS_DW_SCRATCH_FLOATS / (long) n_cols);
-		set_1d(hip_launch_config, (unsigned) grid, 256, (unsigned) lds);
+		set_1d(hip_launch_config, (unsigned) grid, vec ? (unsigned) (slots * tpr) : 256u, (unsigned) lds);
 		return 0;
 	}
 	const int nv = rms_vec_chunks(n_cols, (int) elem, ptr_bits(ARG(op, 4, void *)) | ptr_bits(ARG(op, 5, void *)));
@@ -224,7 +240,8 @@ static int rope_config(Hip_Launch_Config * c, Dataflow_Handle * h, Hip_Function 
 		/* vector path: one workgroup per token at a time, persistent, as many
 		 * per CU as the kernel's registers allow (at most ROPE_SLOT_WG_PER_CU) */
 		grid = MY_MIN((uint64_t) dev(h)->cu_count * ROPE_SLOT_WG_PER_CU, (uint64_t) resident_groups(h, f, ROPE_SLOT_THREADS, 0));
-		grid = MY_MIN(n_tokens, grid);
+		const uint64_t tg = (uint64_t) rope_tokens_per_group(model_dim, num_kv_heads * head_dim, (int) elem);
+		grid = MY_MIN(MY_CEIL(n_tokens, tg), grid);
 		set_1d(c, (unsigned) grid, ROPE_SLOT_THREADS, 0);
 		return 0;
 	}
@@ -340,7 +357,15 @@ static int smx_config(Hip_Launch_Config * c, Dataflow_Handle * h, Hip_Function *
 }
 
 int softmax_set_launch_config(Hip_Launch_Config * hip_launch_config, Dataflow_Handle * dataflow_handle, Hip_Function * hip_function, Op * op) {
-	return smx_config(hip_launch_config, dataflow_handle, hip_function, ARG(op, 0, int), ARG(op, 1, int), "softmax");
+	const int n_rows = ARG(op, 0, int), n_cols = ARG(op, 1, int);
+	if (smx_config(hip_launch_config, dataflow_handle, hip_function, n_rows, n_cols, "softmax")) return -1;
+	/* fp8 logits whose rows fit the registers: two smaller workgroups per CU */
+	if (is_fp8(hip_function, 2) && n_rows > 0 && f8_smx_regs_ok(n_cols) &&
+		((ptr_bits(ARG(op, 2, void *)) | ptr_bits(ARG(op, 3, void *))) & 15ull) == 0) {
+		const long grid = MY_MIN((long) n_rows, 2L * (long) dev(dataflow_handle)->cu_count);
+		set_1d(hip_launch_config, (unsigned) grid, F8_SMX_THREADS, 0);
+	}
+	return 0;
 }
 
 int softmax_cross_entropy_loss_set_launch_config(Hip_Launch_Config * hip_launch_config, Dataflow_Handle * dataflow_handle, Hip_Function * hip_function, Op * op) {

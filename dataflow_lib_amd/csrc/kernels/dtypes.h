@@ -89,18 +89,23 @@ template <> __device__ __forceinline__ R16 pack16<f16_t>(const float * f) {
 /*
  * fp8 storage: the OCP 8-bit formats E4M3 (bias 7, no infinities, max 448)
  * and E5M2 (bias 15, max 57344), which gfx950's conversion instructions
- * implement (v_cvt_f32_fp8 / _bf8 decode, v_cvt_pk_fp8_f32 / _bf8_f32 encode
- * two floats with round to nearest even). Encoding saturates to the largest
+ * implement (v_cvt_pk_f32_fp8 / _bf8 decode two codes, v_cvt_pk_fp8_f32 /
+ * _bf8_f32 encode two floats with round to nearest even; out of range they
+ * give NaN / inf). Encoding saturates to the largest
  * finite value, as the reference's conversions do (CUDA's fp8 constructors
  * from float, __NV_SATFINITE): the input is clamped to +-max first, NaN kept.
  * fp8 is a forward-only storage type.
  */
 struct fp8e4m3_t { uint8_t bits; };
 struct fp8e5m2_t { uint8_t bits; };
+template <typename T> struct IsFp8 { static constexpr bool value = false; };
+template <> struct IsFp8<fp8e4m3_t> { static constexpr bool value = true; };
+template <> struct IsFp8<fp8e5m2_t> { static constexpr bool value = true; };
 
 __device__ __forceinline__ float to_f(fp8e4m3_t x) { return __builtin_amdgcn_cvt_f32_fp8((int) x.bits, 0); }
 __device__ __forceinline__ float to_f(fp8e5m2_t x) { return __builtin_amdgcn_cvt_f32_bf8((int) x.bits, 0); }
 
+typedef float f32x2_t __attribute__((ext_vector_type(2)));
 template <typename T> struct Fp8Traits;
 template <> struct Fp8Traits<fp8e4m3_t> {
 	static constexpr float MAX = 448.0f;
@@ -109,13 +114,11 @@ template <> struct Fp8Traits<fp8e4m3_t> {
 		return hi ? (uint32_t) __builtin_amdgcn_cvt_pk_fp8_f32(a, b, (int) old, true)
 				  : (uint32_t) __builtin_amdgcn_cvt_pk_fp8_f32(a, b, (int) old, false);
 	}
-	__device__ static __forceinline__ float byte(uint32_t w, int k) {
-		switch (k) {
-			case 0: return __builtin_amdgcn_cvt_f32_fp8((int) w, 0);
-			case 1: return __builtin_amdgcn_cvt_f32_fp8((int) w, 1);
-			case 2: return __builtin_amdgcn_cvt_f32_fp8((int) w, 2);
-			default: return __builtin_amdgcn_cvt_f32_fp8((int) w, 3);
-		}
+	/* bytes 0-1 (hi = false) or 2-3 (hi = true) of w, two per instruction */
+	__device__ static __forceinline__ void unpack2(uint32_t w, bool hi, float * f) {
+		const f32x2_t v = hi ? __builtin_amdgcn_cvt_pk_f32_fp8((int) w, true) : __builtin_amdgcn_cvt_pk_f32_fp8((int) w, false);
+		f[0] = v.x;
+		f[1] = v.y;
 	}
 };
 template <> struct Fp8Traits<fp8e5m2_t> {
@@ -124,13 +127,10 @@ template <> struct Fp8Traits<fp8e5m2_t> {
 		return hi ? (uint32_t) __builtin_amdgcn_cvt_pk_bf8_f32(a, b, (int) old, true)
 				  : (uint32_t) __builtin_amdgcn_cvt_pk_bf8_f32(a, b, (int) old, false);
 	}
-	__device__ static __forceinline__ float byte(uint32_t w, int k) {
-		switch (k) {
-			case 0: return __builtin_amdgcn_cvt_f32_bf8((int) w, 0);
-			case 1: return __builtin_amdgcn_cvt_f32_bf8((int) w, 1);
-			case 2: return __builtin_amdgcn_cvt_f32_bf8((int) w, 2);
-			default: return __builtin_amdgcn_cvt_f32_bf8((int) w, 3);
-		}
+	__device__ static __forceinline__ void unpack2(uint32_t w, bool hi, float * f) {
+		const f32x2_t v = hi ? __builtin_amdgcn_cvt_pk_f32_bf8((int) w, true) : __builtin_amdgcn_cvt_pk_f32_bf8((int) w, false);
+		f[0] = v.x;
+		f[1] = v.y;
 	}
 };
 
@@ -148,8 +148,8 @@ __device__ __forceinline__ uint32_t fp8_pack4(float a, float b, float c, float d
 }
 template <typename T>
 __device__ __forceinline__ void fp8_unpack4(uint32_t w, float * f) {
-#pragma unroll
-	for (int k = 0; k < 4; k++) f[k] = Fp8Traits<T>::byte(w, k);
+	Fp8Traits<T>::unpack2(w, false, f);
+	Fp8Traits<T>::unpack2(w, true, f + 2);
 }
 
 template <> __device__ __forceinline__ fp8e4m3_t from_f<fp8e4m3_t>(float f) {
@@ -167,18 +167,32 @@ template <> __device__ __forceinline__ void unpack16<fp8e5m2_t>(const R16 & r, f
 #pragma unroll
 	for (int i = 0; i < 4; i++) fp8_unpack4<fp8e5m2_t>(r.w[i], f + 4 * i);
 }
-template <> __device__ __forceinline__ R16 pack16<fp8e4m3_t>(const float * f) {
-	R16 r;
+/* sixteen floats into sixteen fp8 codes. The clamp to +-max is one v_med3
+ * per element, which maps NaN to -max; NaN is looked for one pair at a time
+ * (one unordered compare per two elements), and only lanes that hold one
+ * redo their chunk with the NaN-keeping clamp. */
+template <typename T>
+__device__ __forceinline__ R16 fp8_pack16(const float * f) {
+	constexpr float m = Fp8Traits<T>::MAX;
+	bool nan = false;
 #pragma unroll
-	for (int i = 0; i < 4; i++) r.w[i] = fp8_pack4<fp8e4m3_t>(f[4 * i], f[4 * i + 1], f[4 * i + 2], f[4 * i + 3]);
+	for (int i = 0; i < 16; i += 2) nan |= __builtin_isunordered(f[i], f[i + 1]);
+	R16 r;
+	if (__builtin_expect(nan, 0)) {
+#pragma unroll
+		for (int i = 0; i < 4; i++) r.w[i] = fp8_pack4<T>(f[4 * i], f[4 * i + 1], f[4 * i + 2], f[4 * i + 3]);
+	}
+	else {
+#pragma unroll
+		for (int i = 0; i < 4; i++) {
+			const uint32_t lo = Fp8Traits<T>::cvt_pk(__builtin_amdgcn_fmed3f(f[4 * i], -m, m), __builtin_amdgcn_fmed3f(f[4 * i + 1], -m, m), 0u, false);
+			r.w[i] = Fp8Traits<T>::cvt_pk(__builtin_amdgcn_fmed3f(f[4 * i + 2], -m, m), __builtin_amdgcn_fmed3f(f[4 * i + 3], -m, m), lo, true);
+		}
+	}
 	return r;
 }
-template <> __device__ __forceinline__ R16 pack16<fp8e5m2_t>(const float * f) {
-	R16 r;
-#pragma unroll
-	for (int i = 0; i < 4; i++) r.w[i] = fp8_pack4<fp8e5m2_t>(f[4 * i], f[4 * i + 1], f[4 * i + 2], f[4 * i + 3]);
-	return r;
-}
+template <> __device__ __forceinline__ R16 pack16<fp8e4m3_t>(const float * f) { return fp8_pack16<fp8e4m3_t>(f); }
+template <> __device__ __forceinline__ R16 pack16<fp8e5m2_t>(const float * f) { return fp8_pack16<fp8e5m2_t>(f); }
 
 /* 8 bytes: eight fp8 elements, or the fp8 half of a mixed fp8 x 16-bit chunk */
 struct __attribute__((aligned(8))) R8 {
@@ -218,6 +232,17 @@ __device__ __forceinline__ bool aligned16(const void * p) { return (((uintptr_t)
 /* Empty register barrier: tells the compiler the 16 bytes may have changed,
  * so values derived from them earlier (unpacked floats) are recomputed from
  * the packed registers instead of being kept alive (and spilled) across a pass. */
+/* Software-pipelined loops wait here, at the top of each step, for every
+ * outstanding vector-memory access (s_waitcnt vmcnt(0): the loads issued one
+ * step ago and the stores of the step before), and only then issue the next
+ * step's loads. Left to itself the compiler placed its wait for this step's
+ * data after the next step's loads (the loads sit under branches), which
+ * waited for those too and serialised the pipeline. */
+__device__ __forceinline__ void vmem_wait_all() {
+	__builtin_amdgcn_s_waitcnt(0x0F70);   /* vmcnt(0); expcnt, lgkmcnt at their maxima */
+	__builtin_amdgcn_sched_barrier(0);
+}
+
 __device__ __forceinline__ void reg_barrier(R16 & r) {
 	__asm__ volatile("" : "+v"(r.w[0]), "+v"(r.w[1]), "+v"(r.w[2]), "+v"(r.w[3]));
 }

@@ -52,6 +52,20 @@
  * of this and what the kernel's registers leave resident */
 #define ROPE_SLOT_WG_PER_CU 4
 
+/* fp8 x 16-bit RMSNorm backward (fp8_ops.hip): rows in 8-element chunks
+ * (8 bytes of each fp8 operand, 16 of each 16-bit one); a row slot of TPR
+ * threads covers a row, thread t owning chunks t + TPR k (k < F8_CPT), so
+ * rows of up to 8 * F8_CPT * 1024 columns take this path. bwd_x: 256-thread
+ * workgroups, F8_BWDX_WG_PER_CU per CU; bwd_w: one workgroup of up to 1024
+ * threads per CU whose slots add their partial rows in LDS. */
+#define F8_CPT 2
+#define F8_BWDX_WG_PER_CU 4
+
+/* fp8 -> 16-bit softmax (fp8_ops.hip): rows of up to 8 * F8_SMX_CH *
+ * F8_SMX_THREADS columns held in registers, two workgroups per CU */
+#define F8_SMX_THREADS 512
+#define F8_SMX_CH 32
+
 /* embedding / copy_to_seq_context: one wave per row, 4 waves per workgroup */
 #define GS_WAVES 4
 
@@ -135,6 +149,27 @@ GEOM_FN int rms_dw_geometry(int n_rows, int n_cols, long elem, int nv, int array
 	*block = (unsigned) (slots * tpr);
 	*lds = (unsigned) bytes;
 	return 0;
+}
+
+/* fp8 x 16-bit RMSNorm backward: threads per row slot for the chunked path,
+ * or 0 when rows must take the element path */
+GEOM_FN int f8_row_tpr(int n_cols) {
+	if (n_cols <= 0 || (n_cols % 8) != 0) return 0;
+	const int t = (n_cols / 8 + F8_CPT - 1) / F8_CPT;
+	const int tpr = ((t + 63) / 64) * 64;
+	return tpr <= 1024 ? tpr : 0;
+}
+
+GEOM_FN int f8_smx_regs_ok(int n_cols) {
+	return n_cols > 0 && (n_cols % 8) == 0 && n_cols / 8 <= F8_SMX_CH * F8_SMX_THREADS;
+}
+
+/* RoPE vector path: tokens per workgroup step. fp8 rows are half as long as
+ * bf16 ones, so two tokens go together when their Q and K chunks fit the
+ * slot's registers. */
+GEOM_FN int rope_tokens_per_group(int model_dim, int kv_dim, int elem_bytes) {
+	if (elem_bytes != 1) return 1;
+	return (2 * (model_dim / 16) <= ROPE_SLOT_THREADS * ROPE_QJ && 2 * (kv_dim / 16) <= ROPE_SLOT_THREADS * ROPE_KJ) ? 2 : 1;
 }
 
 /* RoPE: whether the vector (slot) path applies */

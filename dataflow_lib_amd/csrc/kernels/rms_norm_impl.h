@@ -179,7 +179,7 @@ __device__ __forceinline__ void rms_vector(const RmsArgs & a, int nv, float * ld
 #pragma unroll
 				for (int e = 0; e < V; e++) {
 					const int k = (c * 2 + (e & 1)) & 3;
-					swp[k] = fmaf(xf[e], wf[e], swp[k]);
+					if (!IsFp8<T>::value) swp[k] = fmaf(xf[e], wf[e], swp[k]);   /* fp8: weighted sums are not written */
 					ssp[k] = fmaf(xf[e], xf[e], ssp[k]);
 				}
 			}
@@ -329,13 +329,16 @@ __device__ __forceinline__ void rms_stream(const RmsArgs & a, float * lds) {
 					unpack16<T>(reinterpret_cast<const R16 *>(x)[c], xf);
 					unpack16<T>(reinterpret_cast<const R16 *>(W)[c], wf);
 #pragma unroll
-					for (int e = 0; e < V; e++) { sw = fmaf(xf[e], wf[e], sw); ss = fmaf(xf[e], xf[e], ss); }
+					for (int e = 0; e < V; e++) {
+						if (!IsFp8<T>::value) sw = fmaf(xf[e], wf[e], sw);
+						ss = fmaf(xf[e], xf[e], ss);
+					}
 				}
 			}
 			else if (live) {
 				for (int j = tr; j < n_cols; j += tpr) {
 					const float xf = to_f(x[j]);
-					sw = fmaf(xf, to_f(W[j]), sw);
+					if (!IsFp8<T>::value) sw = fmaf(xf, to_f(W[j]), sw);
 					ss = fmaf(xf, xf, ss);
 				}
 			}

@@ -186,53 +186,72 @@ __device__ __forceinline__ int rope_pair_of(int chunk, int head_dim, bool pow2) 
 	return col >> 1;
 }
 
-/* Vector path: one workgroup of ROPE_SLOT_THREADS per token at a time,
- * persistent over tokens t = block, block + grid, ... The next token's Q and
- * K chunks are loaded, and wave 0 builds its cos/sin table into the other
- * half of a double-buffered LDS table, while this token is rotated and
- * stored; one barrier per token. Rows are addressed through per-row buffer
- * ranges (chunks past a row read zero and store nowhere). */
-template <typename T, bool BWD, bool KV = false>
+/* Vector path: one workgroup of ROPE_SLOT_THREADS per group of TG
+ * consecutive tokens at a time (TG = rope_tokens_per_group: 2 for fp8, whose
+ * rows are half as long, else 1), persistent over groups g = block,
+ * block + grid, ... The group's Q rows (and K rows) are contiguous, so they
+ * are addressed as one span through one buffer range (chunks past the last
+ * token read zero and store nowhere); chunk c of a span belongs to token
+ * c / (row chunks). The next group's Q and K chunks are loaded, and waves
+ * 0..TG-1 build its tokens' cos/sin tables into the other half of a
+ * double-buffered LDS table, while this group is rotated and stored; one
+ * barrier per group. */
+template <typename T, bool BWD, bool KV = false, int TG = 1>
 __device__ __forceinline__ void rope_slot(long n_tokens, int model_dim, int head_dim, int kv_dim, int theta,
 											const int * seq_positions, T * X_q, T * X_k, KvCache<T> kv = KvCache<T>{}) {
+	static_assert(!KV || TG == 1, "the KV-cache scatter runs one token per step");
 	constexpr int VEC = VecOf<T>::N;
 	constexpr int NT = ROPE_SLOT_THREADS;
 	__shared__ float ang[ROPE_MAX_HEAD_DIM / 2];
-	__shared__ __attribute__((aligned(16))) float2 tab[2][ROPE_MAX_HEAD_DIM / 2];
+	__shared__ __attribute__((aligned(16))) float2 tab[2][TG][ROPE_MAX_HEAD_DIM / 2];
 	const int tid = threadIdx.x;
 	const int lane = tid & 63;
-	const bool wave0 = __builtin_amdgcn_readfirstlane(tid >> 6) == 0;
+	const int wv = __builtin_amdgcn_readfirstlane(tid >> 6);
 	const int half = head_dim >> 1;
 
 	const int nvq = model_dim / VEC, nvk = kv_dim / VEC;
 	const uint32_t qbytes = (uint32_t) model_dim * (uint32_t) sizeof(T), kbytes = (uint32_t) kv_dim * (uint32_t) sizeof(T);
 	const bool pow2 = (head_dim & (head_dim - 1)) == 0;
+	const long n_groups = (n_tokens + TG - 1) / TG;
 	/* pair index of each owned chunk: the same in every Q and K row, since
-	 * both rows start at a head boundary */
-	int pr[ROPE_QJ];
+	 * both rows start at a head boundary; and the chunk's token in the group */
+	int pr[ROPE_QJ], tq[ROPE_QJ], tk[ROPE_KJ];
 #pragma unroll
-	for (int j = 0; j < ROPE_QJ; j++) pr[j] = rope_pair_of<T>(tid + NT * j, head_dim, pow2);
+	for (int j = 0; j < ROPE_QJ; j++) {
+		pr[j] = rope_pair_of<T>(tid + NT * j, head_dim, pow2);
+		tq[j] = (TG == 1) ? 0 : (tid + NT * j) / nvq;
+	}
+#pragma unroll
+	for (int j = 0; j < ROPE_KJ; j++) tk[j] = (TG == 1 || nvk == 0) ? 0 : (tid + NT * j) / nvk;
 
-	/* the cos/sin table of token t into tab[b] (wave 0) */
-	auto table = [&](long t, int b) {
+	/* the cos/sin tables of group g's tokens into tab[b] (wave i builds token i) */
+	auto table = [&](long g, int b) {
+		const long t = g * TG + wv;
+		if (wv >= TG || t >= n_tokens) return;
 		const float fpos = (float) load_scalar(seq_positions + t);
 		for (int p = lane; p < half; p += 64) {
 			const float arg = fpos * ang[p];
 			double sd, cd;
 			sincos((double) arg, &sd, &cd);
-			tab[b][p] = make_float2((float) cd, (float) sd);
+			tab[b][wv][p] = make_float2((float) cd, (float) sd);
 		}
 	};
+	/* byte ranges of group g's Q and K spans */
+	auto span = [&](long g, uint32_t row_bytes) {
+		const long left = n_tokens - g * TG;
+		return (uint32_t) (left < TG ? left : TG) * row_bytes;
+	};
 	constexpr int VJ = KV ? ROPE_KJ : 1;
-	auto load = [&](long t, R16 (&q)[ROPE_QJ], R16 (&k)[ROPE_KJ], R16 (&v)[VJ]) {
-		const __amdgpu_buffer_rsrc_t rq = make_rsrc(X_q + t * model_dim, qbytes);
-		const __amdgpu_buffer_rsrc_t rk = make_rsrc(X_k + t * kv_dim, kbytes);
+	auto load = [&](long g, R16 (&q)[ROPE_QJ], R16 (&k)[ROPE_KJ], R16 (&v)[VJ]) {
+		const long t = g * TG;
+		const __amdgpu_buffer_rsrc_t rq = make_rsrc(X_q + t * model_dim, span(g, qbytes));
+		const __amdgpu_buffer_rsrc_t rk = make_rsrc(X_k + t * kv_dim, span(g, kbytes));
 #pragma unroll
 		for (int j = 0; j < ROPE_QJ; j++)
-			if (NT * j < nvq) q[j] = buf_load16_nt(rq, (uint32_t) (tid + NT * j) * 16u, 0);
+			if (NT * j < TG * nvq) q[j] = buf_load16_nt(rq, (uint32_t) (tid + NT * j) * 16u, 0);
 #pragma unroll
 		for (int j = 0; j < ROPE_KJ; j++)
-			if (NT * j < nvk) k[j] = buf_load16_nt(rk, (uint32_t) (tid + NT * j) * 16u, 0);
+			if (NT * j < TG * nvk) k[j] = buf_load16_nt(rk, (uint32_t) (tid + NT * j) * 16u, 0);
 		if (KV) {
 			const __amdgpu_buffer_rsrc_t rv = make_rsrc(kv.values + t * kv_dim, kbytes);
 #pragma unroll
@@ -251,20 +270,20 @@ __device__ __forceinline__ void rope_slot(long n_tokens, int model_dim, int head
 		r = pack16<T>(f);
 	};
 
-	long t = blockIdx.x;
+	long t = blockIdx.x;   /* the group (the token when TG = 1) */
 	const long stride = gridDim.x;
 	R16 q[ROPE_QJ], k[ROPE_KJ], v[VJ];
-	/* the first token's chunks are requested before the angle setup, whose
+	/* the first group's chunks are requested before the angle setup, whose
 	 * fp64 pow latency then overlaps the loads */
-	if (t < n_tokens) load(t, q, k, v);
+	if (t < n_groups) load(t, q, k, v);
 	/* angle_p, exactly as the reference's fp32 expression
 	 * powf(theta, -((float) c / (float) head_dim)) evaluated correctly rounded */
 	for (int p = tid; p < half; p += NT) ang[p] = (float) pow((double) (float) theta, (double) -((float) (2 * p) / (float) head_dim));
 	lds_barrier();   /* angles */
-	if (t < n_tokens && wave0) table(t, 0);
+	if (t < n_groups) table(t, 0);
 	lds_barrier();
 	int b = 0;
-	for (; t < n_tokens; t += stride) {
+	for (; t < n_groups; t += stride) {
 		const long tn = t + stride;
 		/* this token's chunks (requested one token ago) and the previous
 		 * token's stores complete here, before the next token's chunks are
@@ -274,9 +293,9 @@ __device__ __forceinline__ void rope_slot(long n_tokens, int model_dim, int head
 		__builtin_amdgcn_s_waitcnt(0x0F70);   /* vmcnt(0) */
 		__builtin_amdgcn_sched_barrier(0);
 		R16 qn[ROPE_QJ], kn[ROPE_KJ], vn[VJ];
-		if (tn < n_tokens) {
+		if (tn < n_groups) {
 			load(tn, qn, kn, vn);
-			if (wave0) table(tn, b ^ 1);
+			table(tn, b ^ 1);
 		}
 		/* fused KV-cache scatter: this token's context rows (scalar reads) */
 		T * kctx = nullptr;
@@ -285,20 +304,19 @@ __device__ __forceinline__ void rope_slot(long n_tokens, int model_dim, int head
 			kctx = kv.row(t, kv_dim, seq_positions, false);
 			vctx = kv.row(t, kv_dim, seq_positions, true);
 		}
-		const float2 * cs = tab[b];
-		const __amdgpu_buffer_rsrc_t rq = make_rsrc(X_q + t * model_dim, qbytes);
-		const __amdgpu_buffer_rsrc_t rk = make_rsrc(X_k + t * kv_dim, kbytes);
+		const __amdgpu_buffer_rsrc_t rq = make_rsrc(X_q + t * TG * model_dim, span(t, qbytes));
+		const __amdgpu_buffer_rsrc_t rk = make_rsrc(X_k + t * TG * kv_dim, span(t, kbytes));
 #pragma unroll
 		for (int j = 0; j < ROPE_QJ; j++) {
-			if (NT * j < nvq) {
-				rot(q[j], pr[j], cs);
+			if (NT * j < TG * nvq) {
+				rot(q[j], pr[j], tab[b][tq[j] < TG ? tq[j] : 0]);
 				buf_store16_nt(rq, (uint32_t) (tid + NT * j) * 16u, 0, q[j]);
 			}
 		}
 #pragma unroll
 		for (int j = 0; j < ROPE_KJ; j++) {
-			if (NT * j < nvk) {
-				rot(k[j], pr[j], cs);
+			if (NT * j < TG * nvk) {
+				rot(k[j], pr[j], tab[b][tk[j] < TG ? tk[j] : 0]);
 				buf_store16_nt(rk, (uint32_t) (tid + NT * j) * 16u, 0, k[j]);
 			}
 		}
@@ -332,7 +350,7 @@ __device__ __forceinline__ void rope_slot(long n_tokens, int model_dim, int head
 			}
 		}
 		/* tab[b ^ 1] complete, and every read of tab[b] done before it is
-		 * rebuilt; the next token's loads stay in flight across it */
+		 * rebuilt; the next group's loads stay in flight across it */
 		lds_barrier();
 #pragma unroll
 		for (int j = 0; j < ROPE_QJ; j++) q[j] = qn[j];
@@ -352,8 +370,16 @@ __device__ __forceinline__ void rope_dispatch(uint64_t N, int model_dim, int hea
 	const int kv_dim = num_kv_heads * head_dim;
 	unsigned long long ptr_or = (unsigned long long) (uintptr_t) X_q | (unsigned long long) (uintptr_t) X_k;
 	if (KV) ptr_or |= (unsigned long long) (uintptr_t) kv.values;
-	if (blockDim.x == ROPE_SLOT_THREADS && rope_slot_ok(model_dim, kv_dim, head_dim, (int) sizeof(T), ptr_or))
-		rope_slot<T, BWD, KV>((long) (N / (uint64_t) model_dim), model_dim, head_dim, kv_dim, theta, seq_positions, X_q, X_k, kv);
+	if (blockDim.x == ROPE_SLOT_THREADS && rope_slot_ok(model_dim, kv_dim, head_dim, (int) sizeof(T), ptr_or)) {
+		const long n_tokens = (long) (N / (uint64_t) model_dim);
+		if constexpr (!KV && IsFp8<T>::value) {
+			if (rope_tokens_per_group(model_dim, kv_dim, (int) sizeof(T)) == 2) {
+				rope_slot<T, BWD, false, 2>(n_tokens, model_dim, head_dim, kv_dim, theta, seq_positions, X_q, X_k);
+				return;
+			}
+		}
+		rope_slot<T, BWD, KV>(n_tokens, model_dim, head_dim, kv_dim, theta, seq_positions, X_q, X_k, kv);
+	}
 	else
 		rope_impl<T, BWD, KV>(N, model_dim, head_dim, num_kv_heads, theta, seq_positions, X_q, X_k, kv);
 }

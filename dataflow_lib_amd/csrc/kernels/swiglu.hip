@@ -40,8 +40,12 @@ __device__ __forceinline__ float exp_scaled64(float g) {   /* exp(g) * 2^64 */
 	return __builtin_amdgcn_exp2f(fmaf(g, LOG2E_F, 64.0f));
 }
 
+/* DEEP = false drops the deep-negative branch: for fp8 outputs and finite
+ * inputs every result it would produce (|silu(g) u| < 64 e^-64 57344 < 2^-70)
+ * rounds to a zero of the same sign as the fast form's */
+template <bool DEEP = true>
 __device__ __forceinline__ float swiglu_fwd_elem(float g, float u) {
-	if (g < SWIGLU_DEEP_NEG) return ((g * u) * exp_scaled64(g)) * TWO_POW_M64;
+	if (DEEP && g < SWIGLU_DEEP_NEG) return ((g * u) * exp_scaled64(g)) * TWO_POW_M64;
 	return (g * sigmoidf_fast(g)) * u;
 }
 
@@ -63,6 +67,7 @@ __device__ __forceinline__ void swiglu_fwd(long n, const T * g, const T * u, T *
 		if (v < nvec) { gr[k] = ld16_nt(gv + v); ur[k] = ld16_nt(uv + v); }
 	}
 	for (long v0 = tid; v0 < nvec; v0 += nth * SWIGLU_FWD_UNROLL) {
+		vmem_wait_all();
 		R16 gn[SWIGLU_FWD_UNROLL], un[SWIGLU_FWD_UNROLL];
 #pragma unroll
 		for (int k = 0; k < SWIGLU_FWD_UNROLL; k++) {
@@ -77,7 +82,7 @@ __device__ __forceinline__ void swiglu_fwd(long n, const T * g, const T * u, T *
 				unpack16<T>(gr[k], gf);
 				unpack16<T>(ur[k], uf);
 #pragma unroll
-				for (int e = 0; e < VEC; e++) of[e] = swiglu_fwd_elem(gf[e], uf[e]);
+				for (int e = 0; e < VEC; e++) of[e] = swiglu_fwd_elem<!IsFp8<T>::value>(gf[e], uf[e]);
 				st16_nt(ov + v, pack16<T>(of));
 			}
 		}
@@ -85,7 +90,7 @@ __device__ __forceinline__ void swiglu_fwd(long n, const T * g, const T * u, T *
 		for (int k = 0; k < SWIGLU_FWD_UNROLL; k++) { gr[k] = gn[k]; ur[k] = un[k]; }
 	}
 	for (long i = nvec * VEC + tid; i < n; i += nth) {
-		out[i] = from_f<T>(swiglu_fwd_elem(to_f(g[i]), to_f(u[i])));
+		out[i] = from_f<T>(swiglu_fwd_elem<!IsFp8<T>::value>(to_f(g[i]), to_f(u[i])));
 	}
 }
 
@@ -123,6 +128,7 @@ __device__ __forceinline__ void swiglu_bwd(long n, const T * g, const T * u, con
 		if (v < nvec) { gr[k] = ld16_nt(gv + v); ur[k] = ld16_nt(uv + v); dr[k] = ld16_nt(dv + v); }
 	}
 	for (long v0 = tid; v0 < nvec; v0 += nth * SWIGLU_BWD_UNROLL) {
+		vmem_wait_all();
 		R16 gn[SWIGLU_BWD_UNROLL], un[SWIGLU_BWD_UNROLL], dn[SWIGLU_BWD_UNROLL];
 #pragma unroll
 		for (int k = 0; k < SWIGLU_BWD_UNROLL; k++) {

@@ -245,11 +245,20 @@ def rms_dw_depth(dt, n_rows, n_cols, arrays, cu_count, max_lds, aligned=True):
     return rows + (slots - 1) + finish + (1 if dt == FP32 else 0)
 
 
-def rms_dw_fp8_depth(n_rows, n_cols, cu_count):
+def rms_dw_fp8_depth(n_rows, n_cols, cu_count, aligned=True):
     """roundings along the dW reduction of the fp8-input rms_norm_bwd_w
-    (fp8_ops.hip, launch shape in hip_ops_config.c): a workgroup's rows in
-    sequence into its LDS row (fp8 x 16-bit products are exact in fp32), then
-    the same finish pass as the other types"""
-    grid = min(n_rows, cu_count, RMS_DW_SCRATCH_FLOATS // n_cols)
-    rows = -(-n_rows // grid)
-    return rows + (-(-grid // RMS_FIN_GROUPS) + RMS_FIN_GROUPS + 1)
+    (fp8_ops.hip, launch shape in hip_ops_config.c; fp8 x 16-bit products are
+    exact in fp32). Chunked path (aligned rows of a multiple of 8 columns, up
+    to 8 * F8_CPT * 1024): a slot's rows in sequence in registers, the
+    workgroup's slots added in LDS, then the finish pass. Element path: the
+    workgroup's rows in sequence into its LDS row, then the finish pass."""
+    F8_CPT = 2
+    tpr = 0
+    if aligned and n_cols % 8 == 0:
+        t = -(-(n_cols // 8) // F8_CPT)
+        tpr = -(-t // 64) * 64
+        tpr = tpr if tpr <= 1024 else 0
+    slots = max(1, 1024 // tpr) if tpr else 1
+    grid = min(-(-n_rows // slots), cu_count, RMS_DW_SCRATCH_FLOATS // n_cols)
+    rows = -(-n_rows // (grid * slots))
+    return rows + (slots - 1) + (-(-grid // RMS_FIN_GROUPS) + RMS_FIN_GROUPS + 1)
