@@ -167,9 +167,10 @@ GEOM_FN int f8_smx_regs_ok(int n_cols) {
 /* RoPE vector path: tokens per workgroup step. fp8 rows are half as long as
  * bf16 ones, so two tokens go together when their Q and K chunks fit the
  * slot's registers. */
+#define ROPE_TG2_QJ 2   /* Q chunks per thread in a two-token step */
 GEOM_FN int rope_tokens_per_group(int model_dim, int kv_dim, int elem_bytes) {
 	if (elem_bytes != 1) return 1;
-	return (2 * (model_dim / 16) <= ROPE_SLOT_THREADS * ROPE_QJ && 2 * (kv_dim / 16) <= ROPE_SLOT_THREADS * ROPE_KJ) ? 2 : 1;
+	return (2 * (model_dim / 16) <= ROPE_SLOT_THREADS * ROPE_TG2_QJ && 2 * (kv_dim / 16) <= ROPE_SLOT_THREADS * ROPE_KJ) ? 2 : 1;
 }
 
 /* RoPE: whether the vector (slot) path applies */

@@ -196,7 +196,7 @@ __device__ __forceinline__ int rope_pair_of(int chunk, int head_dim, bool pow2) 
  * 0..TG-1 build its tokens' cos/sin tables into the other half of a
  * double-buffered LDS table, while this group is rotated and stored; one
  * barrier per group. */
-template <typename T, bool BWD, bool KV = false, int TG = 1>
+template <typename T, bool BWD, bool KV = false, int TG = 1, int QJ = ROPE_QJ>
 __device__ __forceinline__ void rope_slot(long n_tokens, int model_dim, int head_dim, int kv_dim, int theta,
 											const int * seq_positions, T * X_q, T * X_k, KvCache<T> kv = KvCache<T>{}) {
 	static_assert(!KV || TG == 1, "the KV-cache scatter runs one token per step");
@@ -213,16 +213,23 @@ __device__ __forceinline__ void rope_slot(long n_tokens, int model_dim, int head
 	const uint32_t qbytes = (uint32_t) model_dim * (uint32_t) sizeof(T), kbytes = (uint32_t) kv_dim * (uint32_t) sizeof(T);
 	const bool pow2 = (head_dim & (head_dim - 1)) == 0;
 	const long n_groups = (n_tokens + TG - 1) / TG;
-	/* pair index of each owned chunk: the same in every Q and K row, since
-	 * both rows start at a head boundary; and the chunk's token in the group */
-	int pr[ROPE_QJ], tq[ROPE_QJ], tk[ROPE_KJ];
+	/* table entry of each owned chunk: its pair index (the same in every Q
+	 * and K row, since both rows start at a head boundary) within the table
+	 * of the chunk's token in the group (one index per chunk) */
+	constexpr int TS = ROPE_MAX_HEAD_DIM / 2;
+	int iq[QJ], ik[ROPE_KJ];
 #pragma unroll
-	for (int j = 0; j < ROPE_QJ; j++) {
-		pr[j] = rope_pair_of<T>(tid + NT * j, head_dim, pow2);
-		tq[j] = (TG == 1) ? 0 : (tid + NT * j) / nvq;
+	for (int j = 0; j < QJ; j++) {
+		const int c = tid + NT * j;
+		const int tg = (TG == 1) ? 0 : c / nvq;
+		iq[j] = (tg < TG ? tg : 0) * TS + rope_pair_of<T>(c, head_dim, pow2);
 	}
 #pragma unroll
-	for (int j = 0; j < ROPE_KJ; j++) tk[j] = (TG == 1 || nvk == 0) ? 0 : (tid + NT * j) / nvk;
+	for (int j = 0; j < ROPE_KJ; j++) {
+		const int c = tid + NT * j;
+		const int tg = (TG == 1 || nvk == 0) ? 0 : c / nvk;
+		ik[j] = (tg < TG ? tg : 0) * TS + rope_pair_of<T>(c, head_dim, pow2);
+	}
 
 	/* the cos/sin tables of group g's tokens into tab[b] (wave i builds token i) */
 	auto table = [&](long g, int b) {
@@ -242,12 +249,12 @@ __device__ __forceinline__ void rope_slot(long n_tokens, int model_dim, int head
 		return (uint32_t) (left < TG ? left : TG) * row_bytes;
 	};
 	constexpr int VJ = KV ? ROPE_KJ : 1;
-	auto load = [&](long g, R16 (&q)[ROPE_QJ], R16 (&k)[ROPE_KJ], R16 (&v)[VJ]) {
+	auto load = [&](long g, R16 (&q)[QJ], R16 (&k)[ROPE_KJ], R16 (&v)[VJ]) {
 		const long t = g * TG;
 		const __amdgpu_buffer_rsrc_t rq = make_rsrc(X_q + t * model_dim, span(g, qbytes));
 		const __amdgpu_buffer_rsrc_t rk = make_rsrc(X_k + t * kv_dim, span(g, kbytes));
 #pragma unroll
-		for (int j = 0; j < ROPE_QJ; j++)
+		for (int j = 0; j < QJ; j++)
 			if (NT * j < TG * nvq) q[j] = buf_load16_nt(rq, (uint32_t) (tid + NT * j) * 16u, 0);
 #pragma unroll
 		for (int j = 0; j < ROPE_KJ; j++)
@@ -272,7 +279,7 @@ __device__ __forceinline__ void rope_slot(long n_tokens, int model_dim, int head
 
 	long t = blockIdx.x;   /* the group (the token when TG = 1) */
 	const long stride = gridDim.x;
-	R16 q[ROPE_QJ], k[ROPE_KJ], v[VJ];
+	R16 q[QJ], k[ROPE_KJ], v[VJ];
 	/* the first group's chunks are requested before the angle setup, whose
 	 * fp64 pow latency then overlaps the loads */
 	if (t < n_groups) load(t, q, k, v);
@@ -292,7 +299,7 @@ __device__ __forceinline__ void rope_slot(long n_tokens, int model_dim, int head
 		 * came after the next token's requests and waited for those too) */
 		__builtin_amdgcn_s_waitcnt(0x0F70);   /* vmcnt(0) */
 		__builtin_amdgcn_sched_barrier(0);
-		R16 qn[ROPE_QJ], kn[ROPE_KJ], vn[VJ];
+		R16 qn[QJ], kn[ROPE_KJ], vn[VJ];
 		if (tn < n_groups) {
 			load(tn, qn, kn, vn);
 			table(tn, b ^ 1);
@@ -307,16 +314,16 @@ __device__ __forceinline__ void rope_slot(long n_tokens, int model_dim, int head
 		const __amdgpu_buffer_rsrc_t rq = make_rsrc(X_q + t * TG * model_dim, span(t, qbytes));
 		const __amdgpu_buffer_rsrc_t rk = make_rsrc(X_k + t * TG * kv_dim, span(t, kbytes));
 #pragma unroll
-		for (int j = 0; j < ROPE_QJ; j++) {
+		for (int j = 0; j < QJ; j++) {
 			if (NT * j < TG * nvq) {
-				rot(q[j], pr[j], tab[b][tq[j] < TG ? tq[j] : 0]);
+				rot(q[j], iq[j], &tab[b][0][0]);
 				buf_store16_nt(rq, (uint32_t) (tid + NT * j) * 16u, 0, q[j]);
 			}
 		}
 #pragma unroll
 		for (int j = 0; j < ROPE_KJ; j++) {
 			if (NT * j < TG * nvk) {
-				rot(k[j], pr[j], tab[b][tk[j] < TG ? tk[j] : 0]);
+				rot(k[j], ik[j], &tab[b][0][0]);
 				buf_store16_nt(rk, (uint32_t) (tid + NT * j) * 16u, 0, k[j]);
 			}
 		}
@@ -353,7 +360,7 @@ __device__ __forceinline__ void rope_slot(long n_tokens, int model_dim, int head
 		 * rebuilt; the next group's loads stay in flight across it */
 		lds_barrier();
 #pragma unroll
-		for (int j = 0; j < ROPE_QJ; j++) q[j] = qn[j];
+		for (int j = 0; j < QJ; j++) q[j] = qn[j];
 #pragma unroll
 		for (int j = 0; j < ROPE_KJ; j++) k[j] = kn[j];
 		if (KV) {
@@ -374,7 +381,7 @@ __device__ __forceinline__ void rope_dispatch(uint64_t N, int model_dim, int hea
 		const long n_tokens = (long) (N / (uint64_t) model_dim);
 		if constexpr (!KV && IsFp8<T>::value) {
 			if (rope_tokens_per_group(model_dim, kv_dim, (int) sizeof(T)) == 2) {
-				rope_slot<T, BWD, false, 2>(n_tokens, model_dim, head_dim, kv_dim, theta, seq_positions, X_q, X_k);
+				rope_slot<T, BWD, false, 2, ROPE_TG2_QJ>(n_tokens, model_dim, head_dim, kv_dim, theta, seq_positions, X_q, X_k);
 				return;
 			}
 		}
@@ -415,7 +422,7 @@ ROPE_KV_KERNELS(bf16, bf16_t)
 
 /* fp8 forward only (reference: rope.cu:183-300; rope_bwd_x has no fp8 kernels) */
 #define ROPE_FP8_KERNEL(SUFFIX, T)                                                                                  \
-	extern "C" __global__ void __launch_bounds__(256) rope_##SUFFIX##_kernel(uint64_t N, int model_dim, int head_dim, \
+	extern "C" __global__ void __launch_bounds__(256, ROPE_SLOT_WG_PER_CU) rope_##SUFFIX##_kernel(uint64_t N, int model_dim, int head_dim, \
 			int num_kv_heads, int theta, int * seq_positions, T * X_q, T * X_k) {                                    \
 		rope_dispatch<T, false>(N, model_dim, head_dim, num_kv_heads, theta, seq_positions, X_q, X_k);              \
 	}
