@@ -10,8 +10,45 @@
 #define HOST_MATRIX_THREADS 8
 
 static uint64_t g_state = 42;
+static int g_generator = HOST_MATRIX_RAND_PORTABLE;
 
 void host_matrix_seed(uint64_t seed) { g_state = seed; }
+
+int host_matrix_set_generator(int generator) {
+	if (generator != HOST_MATRIX_RAND_PORTABLE && generator != HOST_MATRIX_RAND_LIBC) {
+		fprintf(stderr, "Error: host matrix: unknown generator %d...\n", generator);
+		return -1;
+	}
+	g_generator = generator;
+	return 0;
+}
+
+/* The reference harnesses' generator (test/create_host_matrix.c:4-29): the
+ * polar method of Marsaglia on the C library's rand(), one value kept back
+ * for the next call. The evaluation types follow that code exactly (the
+ * uniform draws and the square root are fp32, the log ratio fp64), so with
+ * the same srand() seed and the same C library the matrices are identical. */
+static float g_libc_kept;
+static int g_libc_has_kept;
+
+static float libc_polar_normal(float mean, float std) {
+	if (std == 0.0f) return mean;
+	if (g_libc_has_kept) {
+		g_libc_has_kept = 0;
+		return mean + std * g_libc_kept;
+	}
+	float x, y, q;
+	for (;;) {
+		x = (float) ((double) ((float) rand() / (float) RAND_MAX) * 2.0 - 1.0);
+		y = (float) ((double) ((float) rand() / (float) RAND_MAX) * 2.0 - 1.0);
+		q = x * x + y * y;
+		if (q < 1.0f && q != 0.0f) break;
+	}
+	const float f = sqrtf((float) (-2.0 * (double) logf(q) / (double) q));
+	g_libc_kept = y * f;
+	g_libc_has_kept = 1;
+	return mean + std * x * f;
+}
 
 /* splitmix64 (Steele, Lea, Flood 2014) */
 static uint64_t next_u64(void) {
@@ -77,6 +114,10 @@ void * create_rand_host_matrix(uint64_t M, uint64_t N, float mean, float std, Da
 	const uint64_t n = M * N;
 	float * v = f32_buffer(n, "create rand host matrix");
 	if (!v) return NULL;
+	if (g_generator == HOST_MATRIX_RAND_LIBC) {
+		for (uint64_t i = 0; i < n; i++) v[i] = libc_polar_normal(mean, std);
+		return finish_from_f32(v, n, dt, opt_dest, "create rand host matrix");
+	}
 	for (uint64_t i = 0; i < n; i += 2) {
 		double a, b;
 		normal_pair(&a, &b);

@@ -9,11 +9,14 @@
  *
  * Differences from the reference: create_identity_host_matrix zeroes the
  * off-diagonal elements (the reference left them uninitialised), and
- * create_rand_host_matrix draws from a portable generator (splitmix64 and
- * fp64 Box-Muller) seeded with 42 and reseedable through host_matrix_seed,
- * instead of the C library's rand(), so matrices are reproducible across
- * hosts. The generator state is process-wide and not thread-safe, like
- * rand().
+ * create_rand_host_matrix draws by default from a portable generator
+ * (splitmix64 and fp64 Box-Muller) seeded with 42 and reseedable through
+ * host_matrix_seed, so matrices are reproducible across hosts.
+ * host_matrix_set_generator(HOST_MATRIX_RAND_LIBC) switches to the
+ * reference's own generator (Marsaglia's polar method on the C library's
+ * rand(), seeded with srand()), which reproduces the reference harnesses'
+ * matrices bit for bit on the same C library. Generator state is
+ * process-wide and not thread-safe, like rand().
  */
 #ifndef CREATE_HOST_MATRIX_H
 #define CREATE_HOST_MATRIX_H
@@ -37,8 +40,14 @@ void * load_host_matrix_from_file(char * filepath, uint64_t M, uint64_t N, Dataf
 /* create_host_matrix.h:14; 0 or -1 */
 int save_host_matrix(char * filename, void * mat, uint64_t M, uint64_t N, DataflowDatatype dt);
 
-/* No counterpart in the reference: reseed create_rand_host_matrix's generator. */
+/* No counterpart in the reference: reseed create_rand_host_matrix's portable generator. */
 void host_matrix_seed(uint64_t seed);
+
+/* No counterpart in the reference: choose create_rand_host_matrix's generator
+ * (0, or -1 for an unknown value). */
+#define HOST_MATRIX_RAND_PORTABLE 0
+#define HOST_MATRIX_RAND_LIBC 1
+int host_matrix_set_generator(int generator);
 
 #ifdef __cplusplus
 }

@@ -10,8 +10,9 @@
                          the reference's own host C for the op registry, compiled
                          from its sources where they lie under /root/reference
                          (datatype strings, SHA-256 fingerprints, op skeletons, op
-                         table). Built only when /root/reference is present; its
-                         kernels are CUDA for sm_90a and cannot be built here.
+                         table) and its harnesses' random-matrix generator. Built
+                         only when /root/reference is present; its kernels are
+                         CUDA for sm_90a and cannot be built here.
 """
 import os
 import subprocess
@@ -32,6 +33,7 @@ REF_SOURCES = [
     "src/set_ops/src/set_native_op_skeletons.c",
     "src/set_ops/src/set_external_op_skeletons.c",
     "src/table/src/table.c",
+    "src/dataflow_handle/nvidia/test/create_host_matrix.c",
 ]
 # exported registry-path entry points; everything else is local and
 # --gc-sections drops what they do not reach (dataflow_convert_datatype's AVX-512
@@ -44,10 +46,11 @@ REF_EXPORTS = [
     "set_native_rope_bwd_x_skeleton", "set_native_copy_to_seq_context_skeleton", "set_native_swiglu_skeleton",
     "set_native_swiglu_bwd_x_skeleton", "set_native_softmax_skeleton", "set_native_cross_entropy_loss_skeleton",
     "register_native_ops", "set_external_matmul_skeleton", "init_table", "insert_table", "find_table", "remove_table", "destroy_table",
+    "rand_normal",
 ]
 REF_INCLUDES = [
     "include", "src/datatype/include", "src/fingerprint/include", "src/ops/include",
-    "src/set_ops/include", "src/dataflow_handle/include", "src/table/include",
+    "src/set_ops/include", "src/dataflow_handle/include", "src/table/include", "src/dataflow_handle/nvidia/test",
 ]
 
 
@@ -101,7 +104,7 @@ def build_reference_host(verbose=False):
     for inc in REF_INCLUDES:
         cmd += ["-I", os.path.join(REF, inc)]
     cmd += [os.path.join(REF, s) for s in REF_SOURCES]
-    cmd += ["-o", tmp, "-Wl,--gc-sections", "-Wl,--version-script=" + vscript, "-lcrypto"]
+    cmd += ["-o", tmp, "-Wl,--gc-sections", "-Wl,--version-script=" + vscript, "-lcrypto", "-lm"]
     _run(cmd, verbose)
     os.replace(tmp, REF_OUT)
     return REF_OUT

@@ -92,3 +92,56 @@ def test_rand_is_seeded_normal_and_rounds_to_the_type():
     assert abs(z.mean()) < 5 / np.sqrt(n) and abs(z.var() - 1) < 5 * np.sqrt(2 / n)
     assert abs((z ** 3).mean()) < 5 * np.sqrt(15 / n)               # symmetric
     assert abs(np.mean(np.abs(z) < 1) - 0.682689) < 5 * np.sqrt(0.2167 / n)
+
+
+def test_libc_generator_reproduces_the_reference_harness_draws():
+    """host_matrix_set_generator(HOST_MATRIX_RAND_LIBC): the same values, bit
+    for bit, as the reference harnesses' rand_normal (compiled from
+    test/create_host_matrix.c into oracle/_ref) after the same srand(), including
+    the value kept back across calls and std == 0 drawing nothing"""
+    import os
+    from support import REF_HOST_LIB
+    if not os.path.exists(REF_HOST_LIB):
+        pytest.skip("reference host library not built (needs /root/reference)")
+    ref = ctypes.CDLL(REF_HOST_LIB)
+    if not hasattr(ref, "rand_normal"):
+        pytest.skip("reference host library predates rand_normal export")
+    ref.rand_normal.restype = ctypes.c_float
+    ref.rand_normal.argtypes = [ctypes.c_float, ctypes.c_float]
+    libc = ctypes.CDLL("libc.so.6")
+    L.host_matrix_set_generator.argtypes = [ctypes.c_int]
+    assert L.host_matrix_set_generator(7) == -1
+    assert L.host_matrix_set_generator(1) == 0
+    try:
+        libc.srand(1234)
+        a = into(37, 54, FP32)
+        L.create_rand_host_matrix(37, 54, 0.5, 2.0, FP32, ptr(a))
+        libc.srand(1234)
+        e = np.array([ref.rand_normal(0.5, 2.0) for _ in range(a.size)], np.float32)
+        assert np.array_equal(a.ravel().view(np.uint32), e.view(np.uint32))
+        # an odd count keeps one value back for the next matrix, as rand_normal does
+        libc.srand(99)
+        p, q = into(1, 5, FP32), into(1, 7, FP32)
+        L.create_rand_host_matrix(1, 5, 0.0, 1.0, FP32, ptr(p))
+        L.create_rand_host_matrix(1, 7, 0.0, 1.0, FP32, ptr(q))
+        libc.srand(99)
+        e = np.array([ref.rand_normal(0.0, 1.0) for _ in range(12)], np.float32)
+        assert np.array_equal(np.concatenate([p.ravel(), q.ravel()]).view(np.uint32), e.view(np.uint32))
+        # std == 0 gives the mean and consumes no draws
+        libc.srand(5)
+        c, d = into(1, 2, FP32), into(1, 4, FP32)
+        L.create_rand_host_matrix(1, 2, 3.0, 0.0, FP32, ptr(c))
+        L.create_rand_host_matrix(1, 4, 0.0, 1.0, FP32, ptr(d))
+        libc.srand(5)
+        e = np.array([ref.rand_normal(0.0, 1.0) for _ in range(4)], np.float32)
+        assert np.all(c == 3.0) and np.array_equal(d.ravel(), e)
+        # the other types are the same draws rounded to nearest even
+        libc.srand(42)
+        f = into(8, 16, FP32)
+        L.create_rand_host_matrix(8, 16, 0.0, 1.0, FP32, ptr(f))
+        libc.srand(42)
+        h = into(8, 16, BF16)
+        L.create_rand_host_matrix(8, 16, 0.0, 1.0, BF16, ptr(h))
+        assert np.array_equal(h, f32_to_bf16_bits(f))
+    finally:
+        assert L.host_matrix_set_generator(0) == 0
