@@ -17,8 +17,10 @@ Infinity Cache cannot serve repeats. The K timed steps run back to back
 between two events on the launch stream (an event between kernels would add
 several microseconds of stream time to every op). The start event is recorded
 behind the queued warm-up launches, with no host synchronization in between,
-so the GPU is busy when it fires: the timed region is steady state at any K
-(a start from an idle GPU once cost about 0.5 ms, ~25 us per step at K = 20).
+so the GPU is busy when it fires, and an untimed settle phase (every buffer
+set once, then SETTLE_STEPS steps) runs before the warm-up, since the first
+steps after the GPU has idled run ~2 % slower: the timed region is steady
+state at any K.
 `value` = sum of per-op algorithmic bytes / measured step time. Per-op time =
 the average launch duration of K back-to-back launches of that op alone
 (rotating its sets, behind a few queued untimed launches), between two events
@@ -27,7 +29,8 @@ reference-compatible split ops (rms_norm_bwd_x, rms_norm_bwd_w, softmax,
 cross_entropy_loss) and the path's neighbours (embedding gather of 8192 rows
 of a 128256 x 4096 bf16 table; copy_to_seq_context of K, V [8192 x 1024] bf16
 into 4 contexts of 2048 positions; rope_copy_to_seq_context, RoPE fused with
-that scatter, on the config-3 Q, K and those contexts). `transformer_head`:
+that scatter, on the config-3 Q, K and those contexts) and the fp8 variants
+at the same shapes (E4M3 forward tensors, bf16 backward ones). `transformer_head`:
 the loss-path driver
 (submit_transformer_head, training pass) at 4096 tokens x 4096 x 128256, whose
 time is its three hipBLASLt GEMMs (reported in TFLOP/s).
@@ -367,14 +370,18 @@ def build_fp8_extras(h, pool, api):
 # launches queued ahead of every timed batch of one op (and of every copy
 # shape), so that its start event fires while the GPU is busy
 PREROLL = 3
+# untimed steps run before the warm-up (time_ops)
+SETTLE_STEPS = 10
 
 
 def time_ops(h, hip, ops, steps, warmup, batches=5):
     """Time `steps` steps (each op once per step, rotating buffer sets) on one
     stream, with events only at the two ends (an event recorded between
     kernels costs the stream several microseconds, which would be counted as
-    the ops' time). The host synchronizes before the `warmup` steps and after
-    the timed ones; the start event is recorded right behind the queued
+    the ops' time). Every op first runs once on each of its buffer sets and
+    SETTLE_STEPS untimed steps follow (the GPU's first steps after idling run
+    slower); the host synchronizes, queues the `warmup` steps, and
+    synchronizes again after the timed ones; the start event is recorded right behind the queued
     warm-up launches, with no synchronization in between, so it fires when the
     warm-up's last kernel ends and the timed region is steady state whatever
     `steps` is (a start event recorded on an idle GPU charges the ramp from
@@ -384,6 +391,18 @@ def time_ops(h, hip, ops, steps, warmup, batches=5):
     batches; the op's time is the median batch's average launch duration
     (kernel plus the gap to the next launch)."""
     stream = h.stream(0)
+    # settle phase, untimed, before the warm-up: every rotating buffer set of
+    # every op once, then SETTLE_STEPS whole steps. Measured on the MI355X
+    # boxes, the first ~7 steps after the GPU has been idle run ~2 % slower
+    # (20 timed steps after 3 warm-up steps: 0.851 ms per step; after 10, 30
+    # or 60: 0.833-0.837 ms; 100 steps after 3: 0.839 ms), so without it the
+    # step time depended on `steps`.
+    for name, _, runs in ops:
+        for r in runs:
+            assert r() == 0, name
+    for w in range(SETTLE_STEPS):
+        for name, _, runs in ops:
+            assert runs[w % len(runs)]() == 0, name
     h.sync()
     for w in range(warmup):
         for name, _, runs in ops:
