@@ -503,3 +503,71 @@ def test_fp8_mixed_type_functions_reduce_to_the_single_type_ones():
     assert O.oracle_rms_norm_sq_sums(FP8E4M3, n_rows, n_cols, ptr(X8), ptr(ss)) == 0
     xv = fp8_decode_all(FP8E4M3)[X8]
     assert np.allclose(ss, (xv * xv).sum(1), rtol=1e-15)
+
+
+def test_fp8_functions_equal_the_16_bit_ones_on_the_decoded_values():
+    """every fp8 value is exactly a bf16 and an fp16 value, so each fp8
+    oracle function must give the pre-rounding values its 16-bit counterpart
+    gives on the decoded inputs (the storage type enters only through the
+    loads, checked code by code above, and the output rounding, checked here
+    against oracle_round); a wrong operand type or a dropped conversion
+    breaks an equality"""
+    g = rng(71)
+    dec = {dt: fp8_decode_all(dt) for dt in (FP8E4M3, FP8E5M2)}
+    for f8 in (FP8E4M3, FP8E5M2):
+        for b16 in (FP16, BF16):
+            def as16(codes):
+                return to_storage(dec[f8][codes].astype(np.float32), b16)
+            R, C = 5, 48
+            X8 = fp8_encode(f8, g.standard_normal(R * C)).reshape(R, C)
+            W8 = fp8_encode(f8, 1 + 0.02 * g.standard_normal(C))
+            U8 = fp8_encode(f8, g.standard_normal(R * C)).reshape(R, C)
+            dY = to_storage(g.standard_normal((R, C)).astype(np.float32), b16)
+            dW = to_storage(0.1 * g.standard_normal(C).astype(np.float32), b16)
+            rs = (1 + np.abs(g.standard_normal(R))).astype(np.float32)
+            # rms_norm_bwd_w: fp8 X with 16-bit dY / dW
+            a, aa, b, bb = np.empty(C), np.empty(C), np.empty(C), np.empty(C)
+            assert O.oracle_rms_norm_bwd_w2(f8, b16, b16, R, C, ptr(rs), ptr(X8), ptr(dY), ptr(dW), ptr(a), ptr(aa)) == 0
+            assert O.oracle_rms_norm_bwd_w(b16, b16, R, C, ptr(rs), ptr(as16(X8)), ptr(dY), ptr(dW), ptr(b), ptr(bb)) == 0
+            assert np.array_equal(a, b) and np.array_equal(aa, bb)
+            # swiglu_bwd_x: fp8 g, u with 16-bit dO
+            n = R * C
+            out8 = [np.empty(n) for _ in range(3)]
+            out16 = [np.empty(n) for _ in range(3)]
+            assert O.oracle_swiglu_bwd2(f8, b16, n, ptr(X8), ptr(U8), ptr(dY), *[ptr(o) for o in out8]) == 0
+            assert O.oracle_swiglu_bwd(b16, n, ptr(as16(X8)), ptr(as16(U8)), ptr(dY), *[ptr(o) for o in out16]) == 0
+            assert all(np.array_equal(p, q) for p, q in zip(out8, out16))
+            # softmax: fp8 logits, x - max rounded in the output type
+            L8 = fp8_encode(f8, 2.0 * g.standard_normal(R * 300)).reshape(R, 300)
+            y8, y16 = np.empty((R, 300)), np.empty((R, 300))
+            assert O.oracle_softmax(f8, b16, R, 300, ptr(L8), ptr(y8)) == 0
+            assert O.oracle_softmax(b16, b16, R, 300, ptr(as16(L8)), ptr(y16)) == 0
+            assert np.array_equal(y8, y16)
+        # single-type forwards: the pre values equal the bf16 ones on the decoded inputs
+        R, C = 4, 64
+        X8 = fp8_encode(f8, g.standard_normal(R * C)).reshape(R, C)
+        W8 = fp8_encode(f8, 1 + 0.02 * g.standard_normal(C))
+        xb = to_storage(dec[f8][X8].astype(np.float32), BF16)
+        wb = to_storage(dec[f8][W8].astype(np.float32), BF16)
+        p8, p16 = [np.empty((R, C)), np.empty(R), np.empty(R), np.empty(R)], [np.empty((R, C)), np.empty(R), np.empty(R), np.empty(R)]
+        assert O.oracle_rms_norm(f8, R, C, 1e-5, ptr(W8), ptr(X8), *[ptr(o) for o in p8]) == 0
+        assert O.oracle_rms_norm(BF16, R, C, 1e-5, ptr(wb), ptr(xb), *[ptr(o) for o in p16]) == 0
+        assert all(np.array_equal(p, q) for p, q in zip(p8, p16))
+        s8, s16 = np.empty(n), np.empty(n)
+        assert O.oracle_swiglu(f8, n, ptr(X8), ptr(U8), ptr(s8)) == 0
+        assert O.oracle_swiglu(BF16, n, ptr(to_storage(dec[f8][X8].astype(np.float32), BF16)),
+                               ptr(to_storage(dec[f8][U8].astype(np.float32), BF16)), ptr(s16)) == 0
+        assert np.array_equal(s8, s16)
+        T, nq, nkv, hd = 3, 2, 1, 16
+        Q8 = fp8_encode(f8, g.standard_normal(T * nq * hd)).reshape(T, nq * hd)
+        K8 = fp8_encode(f8, g.standard_normal(T * nkv * hd)).reshape(T, nkv * hd)
+        pos = np.array([0, 5, 77], np.int32)
+        q8, k8, q16, k16 = np.empty(Q8.shape), np.empty(K8.shape), np.empty(Q8.shape), np.empty(K8.shape)
+        assert O.oracle_rope(f8, 0, T * nq * hd, nq * hd, hd, nkv, 10000, ptr(pos), ptr(Q8), ptr(K8), ptr(q8), ptr(k8)) == 0
+        assert O.oracle_rope(BF16, 0, T * nq * hd, nq * hd, hd, nkv, 10000, ptr(pos),
+                             ptr(to_storage(dec[f8][Q8].astype(np.float32), BF16)),
+                             ptr(to_storage(dec[f8][K8].astype(np.float32), BF16)), ptr(q16), ptr(k16)) == 0
+        assert np.array_equal(q8, q16) and np.array_equal(k8, k16)
+        # and the fp8 rounding of those values is the fp8 store's
+        for v in (p8[0].ravel()[:50], s8[:50], q8.ravel()[:50]):
+            assert np.array_equal(dec[f8][fp8_encode(f8, v)], np.array([O.oracle_round(x, f8) for x in v]))
