@@ -46,6 +46,7 @@ def oracle():
         L.oracle_embedding.argtypes = [i, i, i, vp, vp, ctypes.c_long, vp]
         L.oracle_copy_to_seq_context.argtypes = [i, ctypes.c_uint64, i, vp, vp, vp, vp, vp]
         L.oracle_rms_norm_bwd_x2.argtypes = [i, i, i, i, vp, vp, vp, vp, vp, vp, vp, vp]
+        L.oracle_rms_norm_bwd_x2_exact.argtypes = [i, i, i, i, vp, vp, vp, vp, vp, vp, vp]
         L.oracle_rms_norm_bwd_w2.argtypes = [i, i, i, i, i, vp, vp, vp, vp, vp, vp]
         L.oracle_rms_norm_sq_sums.argtypes = [i, i, i, vp, vp]
         L.oracle_swiglu_bwd2.argtypes = [i, i, ctypes.c_long, vp, vp, vp, vp, vp, vp]

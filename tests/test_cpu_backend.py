@@ -148,3 +148,84 @@ def test_rope_copy_to_seq_context_through_handle(cpu_handle):
 
 def rng_u8(seed, shape):
     return np.random.default_rng(seed).integers(0, 256, size=shape).astype(np.uint8)
+
+
+FP8S = [api.DATAFLOW_FP8E4M3, api.DATAFLOW_FP8E5M2]
+
+
+def _f8(dt, x):
+    from support import to_storage
+    return to_storage(np.asarray(x, np.float32), dt)
+
+
+@pytest.mark.parametrize("f8", FP8S, ids=["e4m3", "e5m2"])
+@pytest.mark.parametrize("b16", [api.DATAFLOW_FP16, BF16], ids=["fp16", "bf16"])
+def test_fp8_variants_through_handle(cpu_handle, f8, b16):
+    """each of the 22 fp8 functions is found by its fingerprint and gets its
+    arguments in the order the kernels read them: the results equal the
+    oracle's on the same inputs, rounded to the output type"""
+    from support import NP_STORAGE, to_f64
+    h, _ = cpu_handle
+    H = ctypes.byref(h)
+    O = oracle()
+    g = np.random.default_rng(int(f8) * 10 + int(b16))
+    R, C = 3, 32
+    X = _f8(f8, g.standard_normal((R, C)))
+    W = _f8(f8, 1 + 0.02 * g.standard_normal(C))
+    # rms_norm fp8: out in fp8, sum of squares in the statistic slot, weighted sums untouched
+    Y = np.zeros_like(X)
+    ws, ss = np.full(R, -3.0, np.float32), np.zeros(R, np.float32)
+    assert api.submit_rms_norm(H, 0, f8, R, C, 1e-5, ptr(W), ptr(X), ptr(Y), ptr(ws), ptr(ss)) == 0
+    pre, e_ss = np.empty((R, C)), np.empty(R)
+    assert O.oracle_rms_norm(f8, R, C, 1e-5, ptr(W), ptr(X), ptr(pre), None, None, None) == 0
+    assert O.oracle_rms_norm_sq_sums(f8, R, C, ptr(X), ptr(e_ss)) == 0
+    assert np.array_equal(to_f64(Y, f8), to_f64(_f8(f8, pre), f8))
+    assert np.array_equal(ss, e_ss.astype(np.float32)) and np.all(ws == -3.0)
+    # rms_norm_bwd_x / bwd_w with 16-bit backward tensors
+    rs = (1 + np.abs(g.standard_normal(R))).astype(np.float32)
+    wsum = g.standard_normal(R).astype(np.float32)
+    dY = (g.standard_normal((R, C))).astype(np.float32)
+    dY = dY.astype(np.float16) if b16 == api.DATAFLOW_FP16 else f32_to_bf16(dY)
+    dX = np.zeros_like(dY)
+    v = np.empty((R, C))
+    assert api.submit_rms_norm_bwd_x(H, 0, f8, b16, R, C, 1e-5, ptr(wsum), ptr(rs), ptr(W), ptr(X), ptr(dY), ptr(dX)) == 0
+    dX0 = np.zeros_like(dY)
+    assert O.oracle_rms_norm_bwd_x2_exact(f8, b16, R, C, ptr(wsum), ptr(rs), ptr(W), ptr(X), ptr(dY), ptr(dX0), ptr(v)) == 0
+    assert np.array_equal(to_f64(dX, b16), np.array([O.oracle_round(x, b16) for x in v.ravel()]).reshape(R, C))
+    dW = np.zeros(C, NP_STORAGE[b16])
+    assert api.submit_rms_norm_bwd_w(H, 0, f8, b16, R, C, 1e-5, ptr(rs), ptr(X), ptr(dY), ptr(dW)) == 0
+    pw, pa = np.empty(C), np.empty(C)
+    assert O.oracle_rms_norm_bwd_w2(f8, b16, b16, R, C, ptr(rs), ptr(X), ptr(dY), ptr(np.zeros(C, NP_STORAGE[b16])), ptr(pw), ptr(pa)) == 0
+    assert np.array_equal(to_f64(dW, b16), np.array([O.oracle_round(x, b16) for x in pw]))
+    # swiglu fwd (fp8) and bwd (fp8 x 16-bit)
+    U = _f8(f8, g.standard_normal((R, C)))
+    out = np.zeros_like(X)
+    assert api.submit_swiglu(H, 0, f8, R, C, ptr(X), ptr(U), ptr(out)) == 0
+    sp = np.empty((R, C))
+    assert O.oracle_swiglu(f8, R * C, ptr(X), ptr(U), ptr(sp)) == 0
+    assert np.array_equal(to_f64(out, f8), to_f64(_f8(f8, sp), f8))
+    dG, dU = np.zeros_like(dY), np.zeros_like(dY)
+    assert api.submit_swiglu_bwd_x(H, 0, f8, b16, R, C, ptr(X), ptr(U), ptr(dY), ptr(dG), ptr(dU)) == 0
+    eg, eu = np.empty((R, C)), np.empty((R, C))
+    assert O.oracle_swiglu_bwd2(f8, b16, R * C, ptr(X), ptr(U), ptr(dY), ptr(eg), None, ptr(eu)) == 0
+    assert np.array_equal(to_f64(dU, b16), np.array([O.oracle_round(x, b16) for x in eu.ravel()]).reshape(R, C))
+    assert np.array_equal(to_f64(dG, b16), np.array([O.oracle_round(x, b16) for x in eg.ravel()]).reshape(R, C))
+    # softmax fp8 -> 16-bit
+    P = np.zeros((R, C), NP_STORAGE[b16])
+    assert api.submit_softmax(H, 0, f8, b16, R, C, ptr(X), ptr(P)) == 0
+    yp = np.empty((R, C))
+    assert O.oracle_softmax(f8, b16, R, C, ptr(X), ptr(yp)) == 0
+    assert np.array_equal(to_f64(P, b16), np.array([O.oracle_round(x, b16) for x in yp.ravel()]).reshape(R, C))
+    # rope fp8 (forward only)
+    Q, K = _f8(f8, g.standard_normal((2, 16))), _f8(f8, g.standard_normal((2, 8)))
+    pos = np.array([3, 11], np.int32)
+    qv, kv = np.empty(Q.shape), np.empty(K.shape)
+    assert O.oracle_rope(f8, 0, 32, 16, 8, 1, 10000, ptr(pos), ptr(Q), ptr(K), ptr(qv), ptr(kv)) == 0
+    assert api.submit_rope(H, 0, f8, 32, 16, 8, 1, 10000, ptr(pos), ptr(Q), ptr(K)) == 0
+    assert np.array_equal(to_f64(Q, f8), to_f64(_f8(f8, qv), f8)) and np.array_equal(to_f64(K, f8), to_f64(_f8(f8, kv), f8))
+    assert api.submit_rope_bwd_x(H, 0, f8, 32, 16, 8, 1, 10000, ptr(pos), ptr(Q), ptr(K)) == -1
+
+
+def f32_to_bf16(x):
+    from support import f32_to_bf16_bits
+    return f32_to_bf16_bits(x)
