@@ -11,8 +11,9 @@
  * fp8 operand and sixteen of each 16-bit one, so both stay coalesced with one
  * load per operand. Rows or tensors that are not multiples of eight elements,
  * or not aligned to 8 / 16 bytes, take element loops. The arithmetic is the
- * same-type kernels' (bwd_x_elem, swiglu_bwd_elem); the dW partial rows and
- * their finish pass are rms_norm.hip's.
+ * same-type kernels' (swiglu_bwd_elem; bwd_x_elem's formula, with the division
+ * by n taken as a multiplication by 1/n on the chunked path); the dW partial
+ * rows and their finish pass are rms_norm.hip's.
  */
 #include "dtypes.h"
 #include "reduce.h"

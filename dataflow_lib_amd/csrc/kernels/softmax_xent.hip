@@ -408,15 +408,12 @@ __device__ __forceinline__ void smx_regs(int n_rows, int n_cols, const T * X, TO
 		cells_sum2(sd, sx, sslots);
 		/* y = exp(d) / sd as one exp2: exp2(d * log2(e) - log2(sd)) */
 		const float nlog2s = -__builtin_amdgcn_logf(sd);
-		/* in flight here: the next row's loads (issued during the max and sum
-		 * passes; this row's own loads were consumed by the max pass) and
-		 * what remains of the previous row's stores; the next row's LDS part
-		 * and label must have landed before that row reads them */
-		WAIT_VMEM_ALL();
-
 #pragma unroll
 		for (int c = 0; c < SMX_MAXCH; c++) {
-			if (c < nch) {
+			/* every lane issues all SMX_MAXCH stores (chunks past the row lie
+			 * outside its buffer range and store nowhere), so the wait below
+			 * can count them */
+			{
 				R16 o;
 #pragma unroll
 				for (int i = 0; i < 4; i++) {
@@ -441,6 +438,16 @@ __device__ __forceinline__ void smx_regs(int n_rows, int n_cols, const T * X, TO
 				buf_store16_nt(rout, voff, c * cstride, o);
 			}
 		}
+		/* in flight here, oldest first: the rest of the previous row's stores,
+		 * the next row's loads (issued during the max and sum passes) and
+		 * this row's SMX_MAXCH stores. Completions are in order, so waiting
+		 * until at most SMX_MAXCH remain means the next row's LDS part and
+		 * label have landed before that row reads them, while this row's
+		 * stores drain behind it; waiting before the output pass instead held
+		 * the pass up until the LDS part requested during the sum pass had
+		 * arrived. */
+		static_assert(SMX_MAXCH == 16, "the wait below counts SMX_MAXCH stores");
+		__builtin_amdgcn_s_waitcnt(0x4F70);   /* vmcnt(16); expcnt, lgkmcnt at their maxima */
 		if (FUSED && tid == 0 && loss) loss[row] = lab_ok ? (logf(sx) + m - xlab_cell[par]) : __builtin_nanf("");
 		par ^= 1;
 	}
