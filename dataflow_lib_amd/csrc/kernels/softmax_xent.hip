@@ -214,8 +214,8 @@ typedef __attribute__((address_space(3))) void * lds_ptr_t;
  * place, and reaches thread 0 (which writes the loss) through an LDS cell.
  * Each wave prefetches into and reads from its own LDS slice only, so no
  * workgroup barrier guards the buffer, and the reductions' barriers wait for
- * LDS only: the one wait for memory in a row is the one before the output
- * pass. */
+ * LDS only: the one wait for memory in a row comes after its output
+ * stores. */
 template <typename T, typename TO, bool FUSED>
 __device__ __forceinline__ void smx_regs(int n_rows, int n_cols, const T * X, TO * out, const uint32_t * labels, float * loss) {
 	constexpr int VEC = VecOf<T>::N;
