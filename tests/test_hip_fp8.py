@@ -86,7 +86,8 @@ def test_fp8_encode_rounding_and_saturation(hdl, dt):
 
 # ---------------- RMSNorm ----------------
 
-RMS_SHAPES = [(16, 4096), (64, 4096), (7, 8192), (33, 1000), (5, 8), (3, 20000), (8192, 4096), (5, 4099), (9, 4112)]
+RMS_SHAPES = [(16, 4096), (64, 4096), (7, 8192), (33, 1000), (5, 8), (3, 20000), (8192, 4096), (5, 4099), (9, 4112),
+              (1024, 8192), (64, 16384)]
 
 
 def rms_inputs(dt, n_rows, n_cols, seed=1):
@@ -148,7 +149,9 @@ def rms_bwd_inputs(fdt, bdt, n_rows, n_cols, seed=11):
 
 MIXED = [(f, b) for f in F8 for b in B16]
 MIXED_IDS = ["%s_%s" % (IDS[f], IDS[b]) for f, b in MIXED]
-BWD_SHAPES = [(16, 4096), (7, 8192), (33, 1000), (5, 8), (3, 20000), (8192, 4096), (5, 4099)]
+# (32, 16384): the widest rows of the chunked path (TPR 1024); (6, 16392): one chunk past it
+BWD_SHAPES = [(16, 4096), (7, 8192), (33, 1000), (5, 8), (3, 20000), (8192, 4096), (5, 4099), (1024, 8192), (32, 16384),
+              (6, 16392)]
 
 
 @pytest.mark.parametrize("fb", MIXED, ids=MIXED_IDS)
@@ -203,7 +206,8 @@ def test_rms_norm_bwd_w_fp8_too_wide_is_refused(hdl):
 
 # ---------------- RoPE ----------------
 
-ROPE_CASES = [(8192, 32, 8, 128, 500000), (64, 32, 8, 128, 500000), (17, 4, 2, 64, 10000), (9, 3, 1, 96, 500000),
+ROPE_CASES = [(8192, 32, 8, 128, 500000), (256, 64, 8, 128, 500000), (64, 32, 8, 128, 500000), (17, 4, 2, 64, 10000),
+              (9, 8, 2, 256, 10000), (9, 3, 1, 96, 500000),
               (5, 2, 2, 6, 10000), (3, 2, 0, 128, 500000)]
 
 
@@ -240,7 +244,7 @@ def test_rope_bwd_has_no_fp8_variant(hdl):
 
 # ---------------- SwiGLU ----------------
 
-SWIGLU_SHAPES = [(33, 1000), (8, 14336), (1, 7), (3, 5), (1024, 14336), (5, 1003)]
+SWIGLU_SHAPES = [(33, 1000), (8, 14336), (1, 7), (3, 5), (1024, 14336), (5, 1003), (64, 28672)]
 
 
 def swiglu_inputs(fdt, bdt, shape, seed):

@@ -83,6 +83,8 @@ def _ri(lo, hi):
 # rows there, with the next row's loads in flight across each row's reduction
 RMS_SHAPES = [(16, 4096), (64, 4096), (7, 8192), (33, 1000), (5, 8), (3, 20000), (8192, 4096), (5, 4099)]   # 4099: wide ragged rows
 RMS_SHAPES += [(_ri(1, 2000), 8 * _ri(1, 1024)), (_ri(1, 300), _ri(1, 9000)), (_ri(500, 3000), 8 * _ri(200, 700))]
+# Llama-3-70B / 405B hidden sizes: the widest rows of the vector path (TPR 512 and 1024), and one past it
+RMS_SHAPES += [(1024, 8192), (64, 16384), (6, 16392)]
 
 
 def rms_inputs(dt, n_rows, n_cols, seed=1):
@@ -375,6 +377,10 @@ for _ in range(3):
     ROPE_CASES.append((_ri(1, 3000), _nq, _ri(0, _nq), 2 * _ri(1, 128), 500000))
 
 
+# Llama-3-70B and 405B heads; head_dim 256 and the largest accepted, 512
+ROPE_CASES += [(256, 64, 8, 128, 500000), (16, 128, 8, 128, 500000), (9, 8, 2, 256, 10000), (3, 2, 1, 512, 10000)]
+
+
 def rope_inputs(dt, T, nq, nkv, hd, seed=51):
     Q = to_storage(normal(seed, (T, nq * hd)), dt)
     K = to_storage(normal(seed + 1, (T, nkv * hd)), dt)
@@ -506,6 +512,7 @@ def test_rope_copy_to_seq_context(hdl, dt, case):
 # (1024, 14336): every thread runs several grid-stride steps (next step's loads in flight)
 SWIGLU_SHAPES = [(33, 1000), (8, 14336), (1, 7), (3, 5), (1024, 14336)]
 SWIGLU_SHAPES += [(_ri(1, 600), _ri(1, 20000)), (_ri(1, 64), 8 * _ri(1, 2000))]
+SWIGLU_SHAPES += [(64, 28672)]   # Llama-3-70B ffn
 
 
 def swiglu_inputs(dt, shape, seed=71, extremes=False):
