@@ -110,7 +110,11 @@ __device__ __forceinline__ void rms_bwd_x_fp8(int n_rows, int n_cols, const floa
 			F8Row nxt;
 			f8_load_row<true>(row + sl.step, n_rows, sl.cpr, sl.tr, sl.tpr, X8, G16, D16, rs_in, ws_in, nxt);
 			const float r = cur.r, r3 = r * r * r, ws = cur.ws;
-			const long base = (long) row * sl.cpr;
+			/* dX is read and written back: stored at device scope through a
+			 * buffer resource over the row (a slot's tpr is a multiple of 64,
+			 * so a wave's lanes share the row) */
+			const int wrow = __builtin_amdgcn_readfirstlane(row);
+			const __amdgpu_buffer_rsrc_t rd = make_rsrc(D16 + (long) wrow * n_cols, (uint32_t) n_cols * 2u);
 #pragma unroll
 			for (int k = 0; k < F8_CPT; k++) {
 				const int c = sl.tr + k * sl.tpr;
@@ -125,7 +129,7 @@ __device__ __forceinline__ void rms_bwd_x_fp8(int n_rows, int n_cols, const floa
 						const float deriv = wf[k][e] * r - ((xf[e] * r3) * inv_n) * ws;
 						df[e] = df[e] + rnd_to<TB>(gf[e] * rnd_to<TB>(deriv));
 					}
-					st16_nt(D16 + 8 * (base + c), pack16<TB>(df));
+					buf_store16_aux<BUF_AUX_DEV>(rd, (uint32_t) c * 16u, 0, pack16<TB>(df));
 				}
 			}
 			cur = nxt;
