@@ -359,8 +359,10 @@ static int smx_config(Hip_Launch_Config * c, Dataflow_Handle * h, Hip_Function *
 int softmax_set_launch_config(Hip_Launch_Config * hip_launch_config, Dataflow_Handle * dataflow_handle, Hip_Function * hip_function, Op * op) {
 	const int n_rows = ARG(op, 0, int), n_cols = ARG(op, 1, int);
 	if (smx_config(hip_launch_config, dataflow_handle, hip_function, n_rows, n_cols, "softmax")) return -1;
-	/* fp8 logits whose rows fit the registers: two smaller workgroups per CU */
-	if (is_fp8(hip_function, 2) && n_rows > 0 && f8_smx_regs_ok(n_cols) &&
+	/* fp8 logits: long rows keep smx_config's one SMX_THREADS workgroup per CU
+	 * (the next row prefetched into LDS); other rows that fit the registers
+	 * take two smaller workgroups per CU */
+	if (is_fp8(hip_function, 2) && n_rows > 0 && !f8_smx_pf_ok(n_cols) && f8_smx_regs_ok(n_cols) &&
 		((ptr_bits(ARG(op, 2, void *)) | ptr_bits(ARG(op, 3, void *))) & 15ull) == 0) {
 		const long grid = MY_MIN((long) n_rows, 2L * (long) dev(dataflow_handle)->cu_count);
 		set_1d(hip_launch_config, (unsigned) grid, F8_SMX_THREADS, 0);

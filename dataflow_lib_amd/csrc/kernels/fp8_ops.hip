@@ -324,6 +324,107 @@ __device__ __forceinline__ void softmax_fp8_regs(int n_rows, int n_cols, const T
 	}
 }
 
+/* Long rows (f8_smx_pf_ok): one SMX_THREADS workgroup per CU; thread t holds
+ * the row's 8-byte pieces t + SMX_THREADS j (j < F8_PF_PIECES) in registers
+ * while the next row is requested, after this row's max reduction, so that
+ * it lands during this row's sum and output passes: its first half straight
+ * into LDS (16-byte buffer loads with the LDS bit, lane-contiguous; read back
+ * in the 8-byte layout, which takes other waves' loads, hence a barrier
+ * after every wave has waited for its own), its second half into registers
+ * (8-byte loads). The reductions' barriers wait for LDS only (cells_max /
+ * cells_sum2), so the prefetch stays in flight across them. The LDS buffer is
+ * 64 KB, so the two-workgroup register path of shorter rows, compiled into the
+ * same kernel, still fits two workgroups per CU. Pieces past the row end load
+ * zeros and are left out of the max and the sum; their stores fall outside
+ * the row's range and store nothing. */
+template <typename TF, typename TO>
+__device__ __forceinline__ void softmax_fp8_pf(int n_rows, int n_cols, const TF * X, TO * out) {
+	constexpr int nt = SMX_THREADS;
+	constexpr int NP = F8_PF_PIECES;
+	constexpr int NH = NP / 2;    /* pieces per thread through LDS, and through registers */
+	constexpr int NL = NH / 2;    /* 16-byte LDS loads per thread and row */
+	static_assert(NP == 16, "the output pass's wait counts 16 stores");
+	__shared__ __attribute__((aligned(16))) float mslots[SMX_WAVES];
+	__shared__ __attribute__((aligned(16))) float sslots[2 * SMX_WAVES];
+	__shared__ __attribute__((aligned(16))) uint8_t pf[NL * nt * 16];
+	const int np = n_cols / 8;
+	const int tid = (int) threadIdx.x;
+	const int wave_base = tid & ~63;
+	const uint8_t * X8 = reinterpret_cast<const uint8_t *>(X);
+	R8 nx[NH];
+	auto request = [&](int r) {
+		const __amdgpu_buffer_rsrc_t rx = make_rsrc(X8 + (long) r * n_cols, (uint32_t) n_cols);
+#pragma unroll
+		for (int k = 0; k < NL; k++)
+			__builtin_amdgcn_raw_ptr_buffer_load_lds(rx, (lds_ptr_t) &pf[16 * (k * nt + wave_base)], 16, (uint32_t) tid * 16u, k * nt * 16,
+													 0, BUF_AUX_NT);
+#pragma unroll
+		for (int j = 0; j < NH; j++) {
+			const u32x2_v v = __builtin_amdgcn_raw_buffer_load_b64(rx, (uint32_t) (tid + nt * (NH + j)) * 8u, 0, BUF_AUX_NT);
+			nx[j].w[0] = v.x;
+			nx[j].w[1] = v.y;
+		}
+	};
+	int row = blockIdx.x;
+	if (row < n_rows) request(row);
+	vmem_wait_all();
+	cells_barrier();
+	for (; row < n_rows; row += gridDim.x) {
+		R8 cur[NP];
+#pragma unroll
+		for (int j = 0; j < NH; j++) cur[j] = *reinterpret_cast<const R8 *>(&pf[8 * (tid + nt * j)]);
+#pragma unroll
+		for (int j = 0; j < NH; j++) cur[NH + j] = nx[j];
+		WAIT_LDS_ALL();
+		float m = -__builtin_inff();
+#pragma unroll
+		for (int j = 0; j < NP; j++) {
+			if (tid + nt * j < np) {
+				float f[8];
+				unpack8_fp8<TF>(cur[j], f);
+#pragma unroll
+				for (int e = 0; e < 8; e++) m = __builtin_elementwise_maximum(m, f[e]);
+			}
+		}
+		m = cells_max(m, mslots);
+		/* every wave has read its pieces (each waited for its LDS reads
+		 * before the barrier in cells_max): the buffer takes the next row */
+		const int next = row + (int) gridDim.x;
+		if (next < n_rows) request(next);
+#pragma unroll
+		for (int j = 0; j < NP; j++) reg_barrier8(cur[j]);
+		float sd = 0.0f, unused = 0.0f;
+#pragma unroll
+		for (int j = 0; j < NP; j++) {
+			if (tid + nt * j < np) {
+				float f[8];
+				unpack8_fp8<TF>(cur[j], f);
+#pragma unroll
+				for (int e = 0; e < 8; e++) sd += exp_fast(rnd_in<TO>(f[e] - m));
+			}
+		}
+		cells_sum2(sd, unused, sslots);
+		const float nlog2s = -__builtin_amdgcn_logf(sd);
+#pragma unroll
+		for (int j = 0; j < NP; j++) reg_barrier8(cur[j]);
+		const __amdgpu_buffer_rsrc_t ro = make_rsrc(out + (long) row * n_cols, (uint32_t) n_cols * 2u);
+#pragma unroll
+		for (int j = 0; j < NP; j++) {
+			float f[8];
+			unpack8_fp8<TF>(cur[j], f);
+#pragma unroll
+			for (int e = 0; e < 8; e++) f[e] = __builtin_amdgcn_exp2f(fmaf(rnd_in<TO>(f[e] - m), SMX_LOG2E, nlog2s));
+			buf_store16_nt(ro, (uint32_t) (tid + nt * j) * 16u, 0, pack16<TO>(f));
+		}
+		/* the next row's loads were issued before these 16 stores and
+		 * complete first: once at most 16 remain, this wave's part of it has
+		 * landed; the barrier then waits for every wave's */
+		__builtin_amdgcn_s_waitcnt(0x4F70);   /* vmcnt(16) */
+		cells_barrier();
+	}
+	vmem_wait_all();
+}
+
 /* Other rows: three passes per row, the later ones re-reading the row (a
  * row of fp8 is n_cols bytes, so they find it in cache): max, sum exp(d),
  * outputs. In both paths d = rnd_out(x - max), since the reference converts x
@@ -331,6 +432,10 @@ __device__ __forceinline__ void softmax_fp8_regs(int n_rows, int n_cols, const T
 template <typename TF, typename TO>
 __device__ __forceinline__ void softmax_fp8(int n_rows, int n_cols, const TF * X, TO * out) {
 	__shared__ float slots[32];
+	if (blockDim.x == SMX_THREADS && f8_smx_pf_ok(n_cols) && aligned16(X) && aligned16(out)) {
+		softmax_fp8_pf<TF, TO>(n_rows, n_cols, X, out);
+		return;
+	}
 	if (blockDim.x == F8_SMX_THREADS && f8_smx_regs_ok(n_cols) && aligned16(X) && aligned16(out)) {
 		softmax_fp8_regs<TF, TO>(n_rows, n_cols, X, out, slots);
 		return;

@@ -160,6 +160,17 @@ GEOM_FN int f8_row_tpr(int n_cols) {
 	return tpr <= 1024 ? tpr : 0;
 }
 
+/* fp8 -> 16-bit softmax, long rows (fp8_ops.hip, softmax_fp8_pf): one
+ * SMX_THREADS workgroup per CU holding the row in registers (F8_PF_PIECES
+ * 8-byte pieces per thread) while the next row streams in, half into LDS and
+ * half into registers; rows of a multiple of 16 columns from F8_PF_MIN_COLS
+ * up to 8 * F8_PF_PIECES * SMX_THREADS */
+#define F8_PF_PIECES 16
+#define F8_PF_MIN_COLS 32768
+GEOM_FN int f8_smx_pf_ok(int n_cols) {
+	return n_cols >= F8_PF_MIN_COLS && (n_cols % 16) == 0 && n_cols / 8 <= F8_PF_PIECES * SMX_THREADS;
+}
+
 GEOM_FN int f8_smx_regs_ok(int n_cols) {
 	return n_cols > 0 && (n_cols % 8) == 0 && n_cols / 8 <= F8_SMX_CH * F8_SMX_THREADS;
 }

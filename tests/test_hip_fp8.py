@@ -292,7 +292,12 @@ def test_swiglu_bwd_fp8(hdl, fb, shape):
 
 # ---------------- softmax ----------------
 
-SMX_SHAPES = [(4, 128256), (3, 1000), (2, 1001), (2, 140000), (5, 64), (1, 1), (7, 4104)]
+# rows of 32768..131072 columns (a multiple of 16) take the path that prefetches
+# the next row: (300, 32768), (520, 65552) and (260, 128256) give workgroups
+# several rows each (more rows than CUs), 65552 leaves two 8-byte pieces in
+# the register half, (2, 131072) is the longest such row
+SMX_SHAPES = [(4, 128256), (3, 1000), (2, 1001), (2, 140000), (5, 64), (1, 1), (7, 4104),
+              (300, 32768), (520, 65552), (260, 128256), (2, 131072)]
 
 
 @pytest.mark.parametrize("fb", MIXED, ids=MIXED_IDS)
