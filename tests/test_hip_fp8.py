@@ -321,3 +321,28 @@ def test_softmax_fp8(hdl, fb, shape):
         out = d.get(po, shape, NP_STORAGE[bdt])
     check_rounded(out, bdt, pre, what="softmax fp8")
     assert np.allclose(to_f64(out, bdt).sum(axis=1), 1.0, atol=2e-2)
+
+
+@pytest.mark.parametrize("fb", MIXED, ids=MIXED_IDS)
+@pytest.mark.parametrize("shape", [(300, 32768), (600, 4104)], ids=lambda s: "%dx%d" % s)
+def test_softmax_fp8_special_rows(hdl, fb, shape):
+    """workgroups walking several rows (the prefetching path and the
+    two-workgroup path) through an all -inf row, a row with +inf and one with
+    NaN (E4M3 has no infinities: they saturate to -448 / 448)"""
+    from dataflow_lib_amd import api
+    fdt, bdt = fb
+    n_rows, n_cols = shape
+    x = normal(103, shape, std=2.0)
+    x[1, :] = -np.inf
+    x[n_rows // 2, 17] = np.inf
+    x[n_rows - 3, n_cols - 1] = np.nan
+    x[4, ::3] = -np.inf
+    X = to_storage(x, fdt)
+    pre = np.empty(shape)
+    assert oracle().oracle_softmax(fdt, bdt, n_rows, n_cols, ptr(X), ptr(pre)) == 0
+    with Dev(hdl) as d:
+        px, po = d.put(X), d.empty(2 * X.size)
+        assert api.submit_softmax(hdl, 0, fdt, bdt, n_rows, n_cols, px, po) == 0
+        out = d.get(po, shape, NP_STORAGE[bdt])
+    check_rounded(out, bdt, pre, what="softmax fp8, special rows")
+    assert np.isnan(to_f64(out, bdt)[n_rows - 3]).all()
