@@ -412,6 +412,35 @@ def test_rope(hdl, dt, case, bwd):
         check_rounded(gk, dt, kv, what="rope K")
 
 
+@pytest.mark.parametrize("theta", [10000, 500000])
+def test_rope_tables_are_the_correctly_rounded_cos_sin(hdl, theta):
+    """fp32 rows of (1, 0) pairs rotate to exactly (cos, sin) of each pair's
+    angle (the compensated rotation adds c * 1 and -s * 0 exactly), so the
+    output is the kernel's table itself: it must equal the oracle's
+    float(cos(double(pos * angle))) bit for bit, over 65536 positions (up to
+    2^20, whose arguments take the kernel's own reduction, and up to 2^27,
+    whose largest ones take the library's) and all 64 angles of a 128-wide
+    head (the vector path) and of a 96-wide one (the element path)"""
+    from dataflow_lib_amd import api
+    for hd in (128, 96):
+        T = 65536
+        Q = np.zeros((T, hd), np.float32)
+        Q[:, 0::2] = 1.0
+        K = np.zeros((T, 0), np.float32)
+        pos = np.concatenate([np.arange(T // 2), rng(77).integers(0, 1 << 20, size=T // 4),
+                              rng(78).integers(0, 1 << 27, size=T - T // 2 - T // 4)]).astype(np.int32)
+        qv, kv = np.empty(Q.shape), np.empty(K.shape)
+        assert oracle().oracle_rope(FP32, 0, T * hd, hd, hd, 0, theta, ptr(pos), ptr(Q), ptr(K), ptr(qv), ptr(kv)) == 0
+        with Dev(hdl) as d:
+            pq, pk, pp = d.put(Q), d.put(np.zeros(16, np.float32)), d.put(pos)
+            assert api.submit_rope(hdl, 0, FP32, T * hd, hd, hd, 0, theta, pp, pq, pk) == 0
+            gq = d.get(pq, Q.shape, np.float32)
+        want = qv.astype(np.float32)
+        bad = np.flatnonzero(gq.view(np.uint32).ravel() != want.view(np.uint32).ravel())
+        assert bad.size == 0, "hd %d: %d table entries differ; first at %d: got %r, want %r" % (
+            hd, bad.size, bad[0], gq.ravel()[bad[0]], want.ravel()[bad[0]])
+
+
 def test_rope_unaligned(hdl):
     from dataflow_lib_amd import api
     dt, T, nq, nkv, hd, theta = BF16, 6, 4, 2, 128, 500000
