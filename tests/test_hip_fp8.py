@@ -293,11 +293,12 @@ def test_swiglu_bwd_fp8(hdl, fb, shape):
 # ---------------- softmax ----------------
 
 # rows of 32768..131072 columns (a multiple of 16) take the path that prefetches
-# the next row: (300, 32768), (520, 65552) and (260, 128256) give workgroups
-# several rows each (more rows than CUs), 65552 leaves two 8-byte pieces in
-# the register half, (2, 131072) is the longest such row
+# the next row: (300, 32768), (520, 65552), (260, 128256) and (1100, 128256)
+# give workgroups several rows each (more rows than CUs; four or five in the
+# last), 65552 leaves two 8-byte pieces in the register half, (2, 131072) is
+# the longest such row
 SMX_SHAPES = [(4, 128256), (3, 1000), (2, 1001), (2, 140000), (5, 64), (1, 1), (7, 4104),
-              (300, 32768), (520, 65552), (260, 128256), (2, 131072), (5, 65536)]
+              (300, 32768), (520, 65552), (260, 128256), (2, 131072), (5, 65536), (1100, 128256)]
 # logits placed off 16-byte alignment: the element-wise loop (for (5, 65536),
 # with the long-row path's workgroup size)
 SMX_UNALIGNED = ((2, 1001), (5, 65536))
