@@ -36,7 +36,7 @@ NOALLOC_OUT = os.path.join(LIB, "libdataflow_noalloc.so")
 SUBMIT_COST_OUT = os.path.join(LIB, "bench_submit_cost")
 CXX = os.environ.get("CXX", "g++")
 
-C_FLAGS = ["-O2", "-fPIC", "-std=gnu11", "-Wall", "-Wextra", "-Wno-unused-parameter", "-Wno-stringop-truncation",
+C_FLAGS = ["-O2", "-fPIC", "-std=gnu11", "-Wall", "-Wextra", "-Werror=format", "-Wno-unused-parameter", "-Wno-stringop-truncation",
            "-D__HIP_PLATFORM_AMD__", "-I", INCLUDE, "-I", os.path.join(CSRC, "kernels"),
            "-I", os.path.join(ROCM, "include")]
 HIP_LINK = ["-L", os.path.join(ROCM, "lib"), "-lamdhip64", "-Wl,-rpath," + os.path.join(ROCM, "lib")]
@@ -54,7 +54,8 @@ def _run(cmd, verbose):
     err = "\n".join(l for l in res.stderr.splitlines() if not any(n in l for n in noise))
     if res.returncode != 0:
         raise RuntimeError("build step failed (%d): %s\n%s\n%s" % (res.returncode, " ".join(cmd), res.stdout, err))
-    if err.strip() and verbose:
+    # warnings are printed on every build, not only verbose ones
+    if err.strip():
         print(err, file=sys.stderr)
 
 

@@ -355,13 +355,13 @@ static void * hip_alloc_mem(Dataflow_Handle * dataflow_handle, uint64_t size_byt
 	void * p = NULL;
 	HIP_CHECK_RET(hipSetDevice(dataflow_handle->device_id), NULL, "device %d", dataflow_handle->device_id);
 	HIP_CHECK_RET(hipMalloc(&p, (size_t) size_bytes), NULL, "allocating %lu bytes on device %d",
-					dataflow_handle->device_id, (unsigned long) size_bytes);
+					(unsigned long) size_bytes, dataflow_handle->device_id);
 	return p;
 }
 
 static void hip_free_mem(Dataflow_Handle * dataflow_handle, void * dev_ptr) {
 	if (hipSetDevice(dataflow_handle->device_id) != hipSuccess || hipFree(dev_ptr) != hipSuccess) {
-		fprintf(stderr, "hip backend: releasing device memory %p on device %d failed\n", dataflow_handle->device_id, dev_ptr);
+		fprintf(stderr, "hip backend: releasing device memory %p on device %d failed\n", dev_ptr, dataflow_handle->device_id);
 	}
 }
 
@@ -369,7 +369,7 @@ static int hip_set_mem(Dataflow_Handle * dataflow_handle, int stream_id, void * 
 	if (stream_id == -1) {
 		HIP_CHECK_RET(hipSetDevice(dataflow_handle->device_id), -1, "device %d", dataflow_handle->device_id);
 		HIP_CHECK_RET(hipMemset(dev_ptr, val, (size_t) size_bytes), -1, "filling %lu bytes at %p",
-						dev_ptr, (unsigned long) size_bytes);
+						(unsigned long) size_bytes, dev_ptr);
 		return 0;
 	}
 	hipStream_t stream;
@@ -377,14 +377,14 @@ static int hip_set_mem(Dataflow_Handle * dataflow_handle, int stream_id, void * 
 		return -1;
 	}
 	HIP_CHECK_RET(hipMemsetAsync(dev_ptr, val, (size_t) size_bytes, stream), -1, "filling %lu bytes at %p",
-					dev_ptr, (unsigned long) size_bytes);
+					(unsigned long) size_bytes, dev_ptr);
 	return 0;
 }
 
 static int hip_enable_access_to_host_mem(Dataflow_Handle * dataflow_handle, void * host_ptr, uint64_t size_bytes, unsigned int flags) {
 	HIP_CHECK_RET(hipHostRegister(host_ptr, (size_t) size_bytes, flags), -1,
 					"registering host memory %p (%lu bytes, flags %u) for device %d",
-					dataflow_handle->device_id, host_ptr, (unsigned long) size_bytes, flags);
+					host_ptr, (unsigned long) size_bytes, flags, dataflow_handle->device_id);
 	return 0;
 }
 

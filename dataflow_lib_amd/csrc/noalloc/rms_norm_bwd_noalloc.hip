@@ -63,13 +63,27 @@ int query_device(int dev, float ** ptr, int * cu_count, int * max_lds) {
 }
 
 /* the current device's state; queried once per device and kept (a thread
- * that finds another one writing it queries for itself) */
-int device_state(float ** ptr, int * cu_count, int * max_lds) {
+ * that finds another one writing it queries for itself). A stream of another
+ * device is refused: the kernels would be handed this device's scratch
+ * address. */
+int device_state(hipStream_t stream, float ** ptr, int * cu_count, int * max_lds) {
 	int dev = 0;
-	const hipError_t e = hipGetDevice(&dev);
+	hipError_t e = hipGetDevice(&dev);
 	if (e != hipSuccess) {
 		fprintf(stderr, "%s: no current device (%s)\n", kWhat, hipGetErrorString(e));
 		return -1;
+	}
+	if (stream != nullptr) {
+		hipDevice_t sdev = 0;
+		e = hipStreamGetDevice(stream, &sdev);
+		if (e != hipSuccess) {
+			fprintf(stderr, "%s: querying the stream's device failed (%s)\n", kWhat, hipGetErrorString(e));
+			return -1;
+		}
+		if ((int) sdev != dev) {
+			fprintf(stderr, "%s: the stream belongs to device %d, the calling thread's current device is %d\n", kWhat, (int) sdev, dev);
+			return -1;
+		}
 	}
 	DeviceState * d = (dev >= 0 && dev < kMaxDevices) ? &g_devices[dev] : nullptr;
 	if (d && d->state.load(std::memory_order_acquire) == 2) {
@@ -123,7 +137,7 @@ extern "C" int dataflow_rms_norm_bwd_noalloc(hipStream_t stream, DataflowDatatyp
 
 	float * part = nullptr;
 	int cu_count = 0, max_lds = 0;
-	if (device_state(&part, &cu_count, &max_lds)) return -1;
+	if (device_state(stream, &part, &cu_count, &max_lds)) return -1;
 
 	const unsigned long long ptr_or = (unsigned long long) (uintptr_t) rms_weight | (unsigned long long) (uintptr_t) X_inp |
 									  (unsigned long long) (uintptr_t) upstream_dX | (unsigned long long) (uintptr_t) dX;

@@ -35,7 +35,8 @@ extern "C" {
  * DATAFLOW_FP32, DATAFLOW_FP16 or DATAFLOW_BF16. Returns 0 (also for zero
  * rows or columns, with nothing launched), or -1 with a message for an
  * unsupported type, a negative size, rows too long for the LDS, a partial
- * row larger than the scratch (n_cols > 4M), or a failed launch.
+ * row larger than the scratch (n_cols > 4M), a stream of another device
+ * than the current one (hipStreamGetDevice), or a failed launch.
  * Calls no hipMalloc, hipFree or other allocating routine. The first call on
  * a device resolves that device's scratch address once (hipGetSymbolAddress).
  * All calls on one GPU share its scratch: calls that overlap in time on one

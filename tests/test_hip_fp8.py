@@ -350,3 +350,46 @@ def test_softmax_fp8_special_rows(hdl, fb, shape):
         out = d.get(po, shape, NP_STORAGE[bdt])
     check_rounded(out, bdt, pre, what="softmax fp8, special rows")
     assert np.isnan(to_f64(out, bdt)[n_rows - 3]).all()
+
+
+@pytest.mark.parametrize("fb", [(FP8E4M3, BF16), (FP8E5M2, FP16)], ids=["e4m3_bf16", "e5m2_fp16"])
+def test_rms_norm_bwd_w_fp8_on_two_streams_matches_one_stream(hdl, fb):
+    """The fp8 dW ops keep their partial rows in the same module scratch as the
+    16-bit ones, so the handle must order them across streams too: a large
+    fp8 bwd_w on stream 0 followed at once by a small one on stream 1, and a
+    16-bit fused backward on stream 0 followed by a small fp8 bwd_w on
+    stream 1, give the same bits as the same launches one after the other."""
+    from dataflow_lib_amd import api
+    fdt, bdt = fb
+    big, small = (8192, 4096), (64, 4096)
+    Xb, Wb, wsb, rsb, dYb, _ = rms_bwd_inputs(fdt, bdt, big[0], big[1], seed=71)
+    Xs, Ws, wss, rss, dYs, _ = rms_bwd_inputs(fdt, bdt, small[0], small[1], seed=72)
+    # a 16-bit fused backward of the big shape (bdt inputs)
+    X16 = to_storage(normal(73, big), bdt)
+    W16 = to_storage(1.0 + normal(74, (big[1],), std=0.02), bdt)
+    dY16 = to_storage(normal(75, big), bdt)
+    rs16 = (1.0 + 0.01 * normal(76, (big[0],))).astype(np.float32)
+
+    def run(first_fused, stream_small):
+        with Dev(hdl) as d:
+            if first_fused:
+                pa = [d.put(a) for a in (rs16, W16, X16, dY16, np.zeros(big, NP_STORAGE[bdt]))] + [d.put(np.zeros(big[1], np.float32))]
+            else:
+                pa = [d.put(a) for a in (rsb, Xb, dYb)] + [d.put(np.zeros(big[1], NP_STORAGE[bdt]))]
+            pb = [d.put(a) for a in (rss, Xs, dYs)] + [d.put(np.zeros(small[1], NP_STORAGE[bdt]))]
+            hdl.sync()
+            if first_fused:
+                assert api.submit_rms_norm_bwd(hdl, 0, bdt, bdt, big[0], big[1], 1e-5, *pa) == 0
+                out_a = (pa[5], (big[1],), np.float32)
+            else:
+                assert api.submit_rms_norm_bwd_w(hdl, 0, fdt, bdt, big[0], big[1], 1e-5, *pa) == 0
+                out_a = (pa[3], (big[1],), NP_STORAGE[bdt])
+            if stream_small == 0:
+                hdl.sync()
+            assert api.submit_rms_norm_bwd_w(hdl, stream_small, fdt, bdt, small[0], small[1], 1e-5, *pb) == 0
+            return d.get(*out_a), d.get(pb[3], (small[1],), NP_STORAGE[bdt])
+
+    for first_fused in (False, True):
+        ref, two = run(first_fused, 0), run(first_fused, 1)
+        for r, g in zip(ref, two):
+            assert np.array_equal(r.view(np.uint8), g.view(np.uint8))
