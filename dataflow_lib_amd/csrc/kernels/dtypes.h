@@ -307,15 +307,13 @@ __device__ __forceinline__ void buf_store16(__amdgpu_buffer_rsrc_t r, uint32_t v
  * Data touched once is loaded and stored with the streaming hint, so
  * single-use streams do not evict lines that other waves still reuse.
  * BUF_AUX_DEV (device scope, which writes the line through the XCD's L2) is
- * used where a kernel stores to lines it has just read and the gain holds
- * inside a sequence of kernels: the fp8-input RMSNorm bwd_x's dX (measured at
- * 8192 x 4096: 40.8 -> 33.1 us per launch alone; 2.6-2.9 us less per launch
- * inside sequences of seven different ops, so part of the saving alone is
- * write traffic that lands on the kernels after it). The 16-bit RMSNorm
- * backward and RoPE (also read-modify-write) ran faster alone with device
- * scope too (48.5 -> 46.5 us, 30.1 -> 29.7 us) but not inside the training
- * step, where the following kernels slowed by as much, so they keep the
- * streaming hint. */
+ * used where a kernel stores to lines it has just read: the RMSNorm backward
+ * kernels' dX (8192 x 4096 bf16, fused backward 48.6 -> 46.5 us per launch;
+ * fp8-input bwd_x 40.8 -> 33.1 us) and, together with the streaming hint,
+ * RoPE's in-place Q and K (30.2 -> 29.9 us). Part of the saving is write
+ * traffic that drains while the next kernel runs: in a sequence of different
+ * memory-bound ops the ops after these run slower by up to as much (a
+ * sequence of the step's seven ops measured 641 us either way). */
 #define BUF_AUX_NT 2
 #define BUF_AUX_DEV 16
 __device__ __forceinline__ R16 buf_load16_nt(__amdgpu_buffer_rsrc_t r, uint32_t voff, uint32_t soff) {

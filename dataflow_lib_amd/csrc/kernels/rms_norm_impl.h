@@ -236,7 +236,7 @@ __device__ __forceinline__ void rms_vector(const RmsArgs & a, int nv, float * ld
 				unpack16<T>(cur.d[c], df);
 #pragma unroll
 				for (int e = 0; e < V; e++) df[e] = bwd_x_elem<T>(wf[e], xf[e], gf[e], df[e], r, r3, cur.ws, n_cols);
-				buf_store16_nt(ro, voff[c], 0, pack16<T>(df));
+				buf_store16_aux<BUF_AUX_DEV>(ro, voff[c], 0, pack16<T>(df));
 			}
 		}
 		else {
@@ -268,7 +268,7 @@ __device__ __forceinline__ void rms_vector(const RmsArgs & a, int nv, float * ld
 					unpack16<T>(cur.d[c], df);
 #pragma unroll
 					for (int e = 0; e < V; e++) df[e] = df[e] + (r * (gf[e] * wf[e]) - xf[e] * coef);
-					buf_store16_nt(ro, voff[c], 0, pack16<T>(df));
+					buf_store16_aux<BUF_AUX_DEV>(ro, voff[c], 0, pack16<T>(df));
 				}
 			}
 			/* rows past the end loaded zeros and r = 0, so they add nothing */

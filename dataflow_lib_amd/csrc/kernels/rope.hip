@@ -317,14 +317,14 @@ __device__ __forceinline__ void rope_slot(long n_tokens, int model_dim, int head
 		for (int j = 0; j < QJ; j++) {
 			if (NT * j < TG * nvq) {
 				rot(q[j], iq[j], &tab[b][0][0]);
-				buf_store16_nt(rq, (uint32_t) (tid + NT * j) * 16u, 0, q[j]);
+				buf_store16_aux<BUF_AUX_DEV | BUF_AUX_NT>(rq, (uint32_t) (tid + NT * j) * 16u, 0, q[j]);
 			}
 		}
 #pragma unroll
 		for (int j = 0; j < ROPE_KJ; j++) {
 			if (NT * j < TG * nvk) {
 				rot(k[j], ik[j], &tab[b][0][0]);
-				buf_store16_nt(rk, (uint32_t) (tid + NT * j) * 16u, 0, k[j]);
+				buf_store16_aux<BUF_AUX_DEV | BUF_AUX_NT>(rk, (uint32_t) (tid + NT * j) * 16u, 0, k[j]);
 			}
 		}
 		if (KV && kv_dim > 0) {
