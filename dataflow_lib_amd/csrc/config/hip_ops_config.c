@@ -340,6 +340,16 @@ int swiglu_bwd_x_set_launch_config(Hip_Launch_Config * hip_launch_config, Datafl
 
 /* ---------------- softmax / cross-entropy ---------------- */
 
+/* The 16-bit and fp32 softmax kernels (softmax_xent.hip) hand rows out from a
+ * counter in the code object and count finished workgroups there, so the
+ * handle orders them across its streams; the fp8 softmax (fp8_ops.hip) keeps
+ * no launch-wide state. */
+int softmax_set_attribute_config(Dataflow_Handle * dataflow_handle, Hip_Function * hip_function) {
+	(void) dataflow_handle;
+	hip_function->function_config.shares_module_scratch = !is_fp8(hip_function, 2);
+	return 0;
+}
+
 /* one workgroup per row; small rows get a smaller workgroup */
 static int smx_config(Hip_Launch_Config * c, Dataflow_Handle * h, Hip_Function * f, int n_rows, int n_cols, const char * what) {
 	const size_t elem = arg_elem_bytes(f, 2);
@@ -378,15 +388,6 @@ int softmax_cross_entropy_loss_set_launch_config(Hip_Launch_Config * hip_launch_
 		return -1;
 	}
 	return smx_config(hip_launch_config, dataflow_handle, hip_function, ARG(op, 0, int), ARG(op, 1, int), "softmax cross entropy loss");
-}
-
-int softmax_cross_entropy_loss_set_finish_launch_config(Hip_Launch_Config * hip_launch_config, Dataflow_Handle * dataflow_handle, Hip_Function * hip_function, Op * op) {
-	(void) dataflow_handle;
-	(void) hip_function;
-	const int n_rows = ARG(op, 0, int), n_cols = ARG(op, 1, int);
-	const int needed = n_rows > 0 && n_cols > 0 && ARG(op, 4, float *) && ARG(op, 5, float *);
-	set_1d(hip_launch_config, needed ? 1u : 0u, SMX_THREADS, 0);
-	return 0;
 }
 
 int cross_entropy_loss_set_launch_config(Hip_Launch_Config * hip_launch_config, Dataflow_Handle * dataflow_handle, Hip_Function * hip_function, Op * op) {

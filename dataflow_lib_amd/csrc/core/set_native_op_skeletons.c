@@ -30,6 +30,7 @@ typedef struct {
 #define F_S DATAFLOW_FP32_SCALAR
 #define U64_S DATAFLOW_UINT64_SCALAR
 #define RMS_INIT "rms_norm_set_attribute_config"
+#define SMX_INIT "softmax_set_attribute_config"
 
 static const Native_Op_Spec native_op_specs[] = {
 	/* reference set_native_op_skeletons.c:234-270 */
@@ -54,12 +55,12 @@ static const Native_Op_Spec native_op_specs[] = {
 	/* :517-549 (rows, cols, x_w1, x_w3, dOut, dX_w1, dX_w3) */
 	{"swiglu_bwd_x",        NICK_FWD_BWD, 7, {I_S, I_S, ARG_FWD, ARG_FWD, ARG_BWD, ARG_BWD, ARG_BWD}, NULL},
 	/* :551-580 (rows, cols, X, out) */
-	{"softmax",             NICK_FWD_BWD, 4, {I_S, I_S, ARG_FWD, ARG_BWD}, NULL},
+	{"softmax",             NICK_FWD_BWD, 4, {I_S, I_S, ARG_FWD, ARG_BWD}, SMX_INIT},
 	/* :582-611 (rows, cols, pred_logits, labels) */
 	{"cross_entropy_loss",  NICK_BWD,     4, {I_S, I_S, ARG_BWD, DATAFLOW_UINT32}, NULL},
 	/* fused softmax + cross-entropy, no reference counterpart:
 	 * (rows, cols, logits (in place), labels, loss fp32 [rows], mean_loss fp32 [1]) */
-	{"softmax_cross_entropy_loss", NICK_FWD, 6, {I_S, I_S, ARG_FWD, DATAFLOW_UINT32, DATAFLOW_FP32, DATAFLOW_FP32}, NULL},
+	{"softmax_cross_entropy_loss", NICK_FWD, 6, {I_S, I_S, ARG_FWD, DATAFLOW_UINT32, DATAFLOW_FP32, DATAFLOW_FP32}, SMX_INIT},
 	/* RoPE fused with the KV-cache scatter, no reference counterpart: rope's
 	 * 8 args, then values and copy_to_seq_context's context pointers and sizes */
 	{"rope_copy_to_seq_context", NICK_FWD, 11, {U64_S, I_S, I_S, I_S, I_S, DATAFLOW_INT, ARG_FWD, ARG_FWD, ARG_FWD,

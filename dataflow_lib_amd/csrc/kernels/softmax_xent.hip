@@ -19,9 +19,11 @@
  * element is read from HBM once and written once. After the max pass the
  * registers are overwritten with d_j (exact in the storage type), so the
  * output pass needs no recomputation of x - m. exp uses the hardware exp2.
- * mean_loss is summed by a second kernel launched right after on the same
- * stream (fixed order, fp64), so it is deterministic and needs no atomics or
- * device-wide fences.
+ * Rows are handed to the workgroups as they free up (a row counter in the
+ * code object), so every workgroup keeps working until the rows run out
+ * instead of the slowest CU's fixed share setting the kernel's end.
+ * mean_loss is summed by the last workgroup to finish (fixed order, fp64, so
+ * it is deterministic), from per-row losses stored at device scope.
  */
 #include "dtypes.h"
 #include "reduce.h"
@@ -112,21 +114,55 @@ __device__ __forceinline__ void cells_sum2(float & a, float & b, float * cells) 
 	b = sb;
 }
 
-/* mean_loss = sum_r loss[r] / n_rows, summed in fp64 in a fixed order
- * (thread t takes rows t, t + blockDim, ...; then the waves in order). Runs as
- * the op's second kernel, after every row's loss is written. */
-__device__ __forceinline__ void mean_loss_finish(int n_rows, const float * loss, float * mean_loss) {
-	__shared__ double dslots[16];
-	if (blockIdx.x != 0 || !loss || !mean_loss) return;
-	double s = 0.0;
-	for (int r = threadIdx.x; r < n_rows; r += blockDim.x) s += (double) loss[r];
-	for (int off = 32; off > 0; off >>= 1) s += __shfl_xor(s, off);
-	if ((threadIdx.x & 63) == 0) dslots[threadIdx.x >> 6] = s;
-	__syncthreads();
+/* Launch-wide state of the softmax kernels, one copy per loaded code object
+ * (per handle): SMX_TICKETS counts the rows handed out beyond each
+ * workgroup's first two, SMX_DONE the workgroups that have finished. Both
+ * are zero between launches: the last workgroup to finish resets them. The
+ * handle orders these ops across its streams, so two launches never share
+ * them. The two counters sit in different 128-byte lines. */
+#define SMX_TICKETS 0
+#define SMX_DONE 32
+__device__ unsigned int g_smx_sched[64];
+
+/* a row's loss, stored at device scope: the workgroup that sums the mean
+ * loss may run on another XCD, whose L2 does not see this one's lines */
+__device__ __forceinline__ void store_loss(float * loss, int row, float v) {
+	__hip_atomic_store(loss + row, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+/* End of every softmax launch. Each workgroup counts itself done once its
+ * loss stores have completed (thread 0 made them and waits for them); the
+ * last one sums mean_loss = sum_r loss[r] / n_rows in fp64 in a fixed order
+ * (thread t takes rows t, t + blockDim, ...; then the waves in order), reading
+ * the losses at device scope, and resets the counters for the next launch.
+ * No workgroup waits for another. */
+template <bool FUSED>
+__device__ __forceinline__ void smx_launch_end(int n_rows, const float * loss, float * mean_loss) {
+	__shared__ int is_last;
+	__shared__ double dslots[SMX_THREADS / 64];
 	if (threadIdx.x == 0) {
-		double t = 0.0;
-		for (int w = 0; w < (int) (blockDim.x >> 6); w++) t += dslots[w];
-		*mean_loss = (float) (t / (double) n_rows);
+		__asm__ volatile("s_waitcnt vmcnt(0)" ::: "memory");
+		const unsigned d = __hip_atomic_fetch_add(&g_smx_sched[SMX_DONE], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+		is_last = (d == gridDim.x - 1u);
+	}
+	__syncthreads();
+	if (!is_last) return;
+	if (FUSED && loss && mean_loss) {
+		__builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
+		double s = 0.0;
+		for (int r = threadIdx.x; r < n_rows; r += blockDim.x) s += (double) __hip_atomic_load(loss + r, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+		for (int off = 32; off > 0; off >>= 1) s += __shfl_xor(s, off);
+		if ((threadIdx.x & 63) == 0) dslots[threadIdx.x >> 6] = s;
+		__syncthreads();
+		if (threadIdx.x == 0) {
+			double t = 0.0;
+			for (int w = 0; w < (int) (blockDim.x >> 6); w++) t += dslots[w];
+			*mean_loss = (float) (t / (double) n_rows);
+		}
+	}
+	if (threadIdx.x == 0) {
+		__hip_atomic_store(&g_smx_sched[SMX_TICKETS], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+		__hip_atomic_store(&g_smx_sched[SMX_DONE], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 	}
 }
 
@@ -281,7 +317,17 @@ __device__ __forceinline__ void smx_regs(int n_rows, int n_cols, const T * X, TO
 		fetch_label(row);
 	}
 	WAIT_VMEM_ALL();
-	for (; row < n_rows; row += gridDim.x) {
+	/* Rows: each workgroup's first two are block and block + grid; every later
+	 * one is a ticket t of the launch's row counter, row 2 * grid + t. The
+	 * ticket for the row after next is taken at the top of each row (thread 0;
+	 * its reply is in well before the sum pass) and published to the other
+	 * waves with the sum reduction's barrier, so the next row's index is known
+	 * when its prefetch starts in the max pass. */
+	__shared__ int nextcell[2];
+	int next = row + (int) gridDim.x;
+	while (row < n_rows) {
+		unsigned ticket = 0u;
+		if (tid == 0 && next < n_rows) ticket = __hip_atomic_fetch_add(&g_smx_sched[SMX_TICKETS], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 		const __amdgpu_buffer_rsrc_t rout = make_rsrc(out + (long) row * n_cols, row_bytes);
 		/* this row: its label and the LDS part (landed: checked before the last
 		 * output pass) and the register part loaded during the last row */
@@ -300,7 +346,6 @@ __device__ __forceinline__ void smx_regs(int n_rows, int n_cols, const T * X, TO
 				if (c < nch) xr[c] = buf_load16_nt(rin, voff, c * cstride);
 		}
 		/* the next row (requested during the max pass) and its label */
-		const int next = row + gridDim.x;
 		const bool has_next = next < n_rows;
 		const bool lab_ok = FUSED && lab < (uint32_t) n_cols;
 		const __amdgpu_buffer_rsrc_t rn = make_rsrc(X + (long) next * n_cols, has_next ? row_bytes : 0u);
@@ -342,7 +387,10 @@ __device__ __forceinline__ void smx_regs(int n_rows, int n_cols, const T * X, TO
 		 * while the memory pipeline accepts them. For the loss, sx is summed
 		 * in the same pass online: so = sum exp(x - mref) against the running
 		 * max (mref = 0 while that is still -inf), rescaled when the max
-		 * grows. */
+		 * grows. (Summing it in the sum pass instead, from exp(d) corrected
+		 * for the rounding of x - m, measured 7 us faster to first order but
+		 * misses the 1e-4 loss bound on confident rows, and 28 us slower to
+		 * second order: that pass is already the kernel's busiest.) */
 		float m = -__builtin_inff();
 		float mref = 0.0f, so = 0.0f;
 #pragma unroll
@@ -405,7 +453,12 @@ __device__ __forceinline__ void smx_regs(int n_rows, int n_cols, const T * X, TO
 		}
 		float sd = sd0 + sd1;
 		float sx = SX ? so : sd;
+		if (tid == 0) {
+			const long r2 = 2L * (long) gridDim.x + (long) ticket;
+			nextcell[par] = (next < n_rows && r2 < (long) n_rows) ? (int) r2 : n_rows;
+		}
 		cells_sum2(sd, sx, sslots);
+		const int next2 = __builtin_amdgcn_readfirstlane(nextcell[par]);
 		/* y = exp(d) / sd as one exp2: exp2(d * log2(e) - log2(sd)) */
 		const float nlog2s = -__builtin_amdgcn_logf(sd);
 #pragma unroll
@@ -448,8 +501,10 @@ __device__ __forceinline__ void smx_regs(int n_rows, int n_cols, const T * X, TO
 		 * arrived. */
 		static_assert(SMX_MAXCH == 16, "the wait below counts SMX_MAXCH stores");
 		__builtin_amdgcn_s_waitcnt(0x4F70);   /* vmcnt(16); expcnt, lgkmcnt at their maxima */
-		if (FUSED && tid == 0 && loss) loss[row] = lab_ok ? (logf(sx) + m - xlab_cell[par]) : __builtin_nanf("");
+		if (FUSED && tid == 0 && loss) store_loss(loss, row, lab_ok ? (logf(sx) + m - xlab_cell[par]) : __builtin_nanf(""));
 		par ^= 1;
+		row = next;
+		next = next2;
 	}
 	WAIT_VMEM_ALL();
 }
@@ -487,7 +542,7 @@ __device__ __forceinline__ void smx_stream(int n_rows, int n_cols, const T * X, 
 			orow[j] = from_f<TO>(y);
 		}
 		if (FUSED && tid == 0 && loss) {
-			loss[row] = (lab < (uint32_t) n_cols) ? (logf(sx) + m - x_lab) : __builtin_nanf("");
+			store_loss(loss, row, (lab < (uint32_t) n_cols) ? (logf(sx) + m - x_lab) : __builtin_nanf(""));
 		}
 		__syncthreads();
 	}
@@ -599,7 +654,7 @@ __device__ __forceinline__ void smx_stream_vec(int n_rows, int n_cols, const T *
 				buf_store16_nt(rout, (uint32_t) c * 16u, 0, o);
 			}
 		}
-		if (FUSED && tid == 0 && loss) loss[row] = lab_ok ? (logf(sx) + mx - xlab_cell) : __builtin_nanf("");
+		if (FUSED && tid == 0 && loss) store_loss(loss, row, lab_ok ? (logf(sx) + mx - xlab_cell) : __builtin_nanf(""));
 		__syncthreads();   /* the cells are rewritten for the next row */
 	}
 }
@@ -613,6 +668,7 @@ __device__ __forceinline__ void smx(int n_rows, int n_cols, const T * X, TO * ou
 	else if (sizeof(TO) == sizeof(T) && n_cols % VEC == 0 && aligned16(X) && aligned16(out) && blockDim.x == SMX_THREADS)
 		smx_stream_vec<T, FUSED>(n_rows, n_cols, X, reinterpret_cast<T *>(out), labels, loss);
 	else smx_stream<T, TO, FUSED>(n_rows, n_cols, X, out, labels, loss);
+	smx_launch_end<FUSED>(n_rows, loss, mean_loss);
 }
 
 #define SMX_KERNELS(SUFFIX, PSUFFIX, T)                                                                                \
@@ -623,10 +679,6 @@ __device__ __forceinline__ void smx(int n_rows, int n_cols, const T * X, TO * ou
 	extern "C" __global__ void __launch_bounds__(SMX_THREADS) softmax_cross_entropy_loss_##SUFFIX##_kernel(int n_rows, \
 			int n_cols, T * logits, uint32_t * labels, float * loss, float * mean_loss) {                              \
 		smx<T, T, true>(n_rows, n_cols, logits, logits, labels, loss, mean_loss);                                      \
-	}                                                                                                                  \
-	extern "C" __global__ void __launch_bounds__(SMX_THREADS) softmax_cross_entropy_loss_##SUFFIX##_kernel_finish(      \
-			int n_rows, int n_cols, T * logits, uint32_t * labels, float * loss, float * mean_loss) {                  \
-		mean_loss_finish(n_rows, loss, mean_loss);                                                                     \
 	}                                                                                                                  \
 	extern "C" __global__ void __launch_bounds__(256) cross_entropy_loss_##SUFFIX##_kernel(int n_rows, int n_cols,     \
 			T * pred_logits, uint32_t * labels) {                                                                      \

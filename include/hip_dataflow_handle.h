@@ -99,13 +99,14 @@ typedef int (*Hip_Set_Func_Attribute)(Dataflow_Handle * dataflow_handle, Hip_Fun
 
 /* What Dataflow_Handle.ctx points to (HIP has no per-handle contexts; the
  * CUDA backend keeps its CUcontext there). The device id comes first, so ctx
- * still reads as the device id. Functions flagged shares_module_scratch (the
- * RMSNorm dW ops) keep per-launch partial results in their code object's
- * module-scope scratch, so the handle orders them across its streams: such
- * an op submitted on another stream than the previous one first waits for
- * everything then queued on that stream (an event recorded only when the
- * stream changes, so single-stream use pays nothing). Other ops, the fused
- * cross-entropy's two kernels included, are not ordered. */
+ * still reads as the device id. Functions flagged shares_module_scratch keep
+ * per-launch state in their code object's module-scope memory (the RMSNorm
+ * dW ops their partial rows; the 16-bit and fp32 softmax and fused
+ * cross-entropy their row counter and finished-workgroup count), so the
+ * handle orders them across its streams: such an op submitted on another
+ * stream than the previous one first waits for everything then queued on
+ * that stream (an event recorded only when the stream changes, so
+ * single-stream use pays nothing). Other ops are not ordered. */
 #define HIP_NO_STREAM INT_MIN
 typedef struct hip_context {
 	int device_id;

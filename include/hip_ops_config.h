@@ -1,7 +1,7 @@
 /*
  * ABI of the launch-configuration library (dlopen'ed by the HIP backend).
- * One "<op>_set_launch_config" per op family, plus the attribute init of the
- * RMSNorm family (reference: src/ops/nvidia/include/nvidia_ops_config.h:9-27).
+ * One "<op>_set_launch_config" per op family, plus the attribute inits of the
+ * RMSNorm and softmax families (reference: src/ops/nvidia/include/nvidia_ops_config.h:9-27).
  * Each returns 0, or -1 when the op cannot be launched for these arguments.
  */
 #ifndef HIP_OPS_CONFIG_H
@@ -43,7 +43,9 @@ int softmax_set_launch_config(Hip_Launch_Config * hip_launch_config, Dataflow_Ha
 int cross_entropy_loss_set_launch_config(Hip_Launch_Config * hip_launch_config, Dataflow_Handle * dataflow_handle, Hip_Function * hip_function, Op * op);
 /* fused softmax + cross-entropy (no reference counterpart) */
 int softmax_cross_entropy_loss_set_launch_config(Hip_Launch_Config * hip_launch_config, Dataflow_Handle * dataflow_handle, Hip_Function * hip_function, Op * op);
-int softmax_cross_entropy_loss_set_finish_launch_config(Hip_Launch_Config * hip_launch_config, Dataflow_Handle * dataflow_handle, Hip_Function * hip_function, Op * op);
+/* attribute init of softmax and the fused op: flags the kernels that keep
+ * launch-wide state in the code object (shares_module_scratch) */
+int softmax_set_attribute_config(Dataflow_Handle * dataflow_handle, Hip_Function * hip_function);
 
 #ifdef __cplusplus
 }

@@ -278,3 +278,17 @@ def rms_dw_fp8_depth(n_rows, n_cols, cu_count, aligned=True):
     grid = min(-(-n_rows // slots), cu_count, RMS_DW_SCRATCH_FLOATS // n_cols)
     rows = -(-n_rows // (grid * slots))
     return rows + (slots - 1) + (-(-grid // RMS_FIN_GROUPS) + RMS_FIN_GROUPS + 1)
+
+
+def confident_logits(shape, seed):
+    """bf16 logits of a confident model: the label holds the row max 7.03125
+    and every other logit sits near 13 below it (N(-13, 0.3)), so about a
+    fifth of sum exp(x - m) comes from the bulk, whose differences x - m are
+    rounded to bf16 with errors up to 2^-5. A loss built from exp(rnd(x - m))
+    corrected only to first order is off by ~2e-4 relative here (the losses
+    are ~0.27); to second order by <1e-6. Returns (bf16 bits, labels)."""
+    n_rows, n_cols = shape
+    x = 7.03125 - 13.0 + normal(seed, shape, std=0.3)
+    labels = rng(seed + 1).integers(0, n_cols, size=n_rows).astype(np.uint32)
+    x[np.arange(n_rows), labels] = 7.03125
+    return to_storage(x, BF16), labels

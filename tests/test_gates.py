@@ -8,7 +8,8 @@ columns). No GPU involved."""
 import numpy as np
 import pytest
 
-from support import BF16, FP32, U32, bf16_bits_to_f32, check_f32, gamma, normal, oracle, ptr, sum_gate, to_storage
+from support import (BF16, FP32, U32, bf16_bits_to_f32, check_f32, confident_logits, gamma, normal, oracle, ptr, sum_gate,
+                     to_storage)
 
 N_ROWS, N_COLS, GROUPS = 8192, 4096, 256
 
@@ -63,3 +64,29 @@ def test_sum_gate_rejects_fp16_partial_rows(config2):
     # shape) is too wide to see it on many of those columns
     loose = 1e-5 * np.abs(dw_pre) + gamma(65) * dw_abs
     assert (np.abs(dw - dw_pre) > loose).mean() < (np.abs(dw - dw_pre) > tol).mean()
+
+
+def test_loss_gate_rejects_a_first_order_loss_sum():
+    """The fused loss kernel sums exp(x - m) over the unrounded differences
+    itself. A cheaper sum built from the softmax's exp(d), d = bf16(x - m),
+    corrected in dl = (x - m) - d, must fail the GPU tests' 1e-4 loss gate on
+    confident rows (support.confident_logits) when the correction stops at
+    first order, and pass it at second order: CPU models of both against the
+    oracle."""
+    shape = (64, 128256)
+    X, labels = confident_logits(shape, 710)
+    n_rows, n_cols = shape
+    lo, hi, loss, mean = np.empty(shape), np.empty(shape), np.empty(n_rows), np.zeros(1)
+    assert oracle().oracle_softmax_cross_entropy(BF16, n_rows, n_cols, ptr(X), ptr(labels), ptr(lo), ptr(hi), ptr(loss),
+                                                 ptr(mean)) == 0
+    x = bf16_bits_to_f32(X).astype(np.float64)
+    m = x.max(axis=1, keepdims=True)
+    e = x - m
+    d = bf16_bits_to_f32(to_storage(e.astype(np.float32), BF16)).astype(np.float64)
+    dl = e - d
+    xl = e[np.arange(n_rows), labels]
+    second = np.log((np.exp(d) * (1.0 + dl + 0.5 * dl * dl)).sum(axis=1)) - xl
+    first = np.log((np.exp(d) * (1.0 + dl)).sum(axis=1)) - xl
+    check_f32(second.astype(np.float32), loss, rel=1e-4, what="second-order loss model")
+    with pytest.raises(AssertionError):
+        check_f32(first.astype(np.float32), loss, rel=1e-4, what="first-order loss model")

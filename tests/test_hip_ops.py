@@ -15,8 +15,8 @@ import ctypes
 import numpy as np
 import pytest
 
-from support import (BF16, FP16, FP32, NP_STORAGE, check_f32, check_rounded, gamma, normal, oracle, ptr, rms_dw_depth,
-                     rms_ws_depth, rng, sum_gate, to_f64, to_storage)
+from support import (BF16, FP16, FP32, NP_STORAGE, check_f32, check_rounded, confident_logits, gamma, normal, oracle, ptr,
+                     rms_dw_depth, rms_ws_depth, rng, sum_gate, to_f64, to_storage)
 
 pytestmark = pytest.mark.gpu
 DTS = [FP32, FP16, BF16]
@@ -333,8 +333,9 @@ def test_dw_ops_on_two_streams_match_one_stream(hdl):
 
 
 def test_fused_cross_entropy_on_two_streams_matches_one_stream(hdl):
-    """The fused loss op is a two-kernel op (its mean loss is a second,
-    deterministic kernel over the rows' losses), which the handle orders
+    """The fused loss op keeps launch-wide state in the code object (the row
+    counter that hands rows to workgroups and the count of finished
+    workgroups, the last of which sums the mean loss), so the handle orders it
     across its streams: launches alternating between two streams without
     waits give the same bits (loss, mean and dlogits) as the same launches on
     one stream, over several rounds."""
@@ -735,6 +736,82 @@ def test_softmax_many_rows(hdl, dt, shape):
         assert api.submit_softmax(hdl, 0, dt, dt, n_rows, n_cols, px, po) == 0
         out = d.get(po, shape, NP_STORAGE[dt])
     check_rounded(out, dt, pre, what="softmax, many rows")
+
+
+def test_fused_loss_on_confident_rows(hdl):
+    """Rows where the label holds the max and the rest of the vocabulary
+    sits ~13 below it (support.confident_logits), so the loss is small and
+    the part of its sum that the bf16 rounding of x - m touches is large: a
+    loss sum built from exp(rnd(x - m)) corrected only to first order misses
+    the 1e-4 gate here (test_gates.py)."""
+    from dataflow_lib_amd import api
+    shape = (300, 128256)
+    X, labels = confident_logits(shape, 720)
+    n_rows, n_cols = shape
+    lo, hi, loss, mean = np.empty(shape), np.empty(shape), np.empty(n_rows), np.zeros(1)
+    assert oracle().oracle_softmax_cross_entropy(BF16, n_rows, n_cols, ptr(X), ptr(labels), ptr(lo), ptr(hi),
+                                                 ptr(loss), ptr(mean)) == 0
+    with Dev(hdl) as d:
+        px, pl, ploss, pmean = d.put(X), d.put(labels), d.empty(4 * n_rows), d.empty(4)
+        assert api.submit_softmax_cross_entropy_loss(hdl, 0, BF16, n_rows, n_cols, px, pl, ploss, pmean) == 0
+        out = d.get(px, shape, NP_STORAGE[BF16])
+        gl = d.get(ploss, (n_rows,), np.float32)
+        gm = d.get(pmean, (1,), np.float32)
+    check_rounded(out, BF16, lo, hi, what="fused dlogits, confident rows")
+    check_f32(gl, loss, rel=1e-4, what="fused loss, confident rows")
+    check_f32(gm, mean, rel=1e-4, what="fused mean loss, confident rows")
+
+
+def test_softmax_row_counter_across_launches(hdl):
+    """The 16-bit and fp32 softmax kernels hand rows past each workgroup's
+    first two out from a counter in the code object, and the last workgroup
+    of a launch resets it. Back-to-back launches of softmax and the fused op
+    in three types and shapes with more rows than two per workgroup, small
+    grids between large ones, register and streaming paths, all queued on one
+    stream with no host synchronization between them, must each match the
+    oracle (a counter left over from one launch would skip or repeat rows of
+    the next)."""
+    from dataflow_lib_amd import api
+    cases = [(BF16, True, (1100, 32000)), (FP32, False, (700, 8000)), (BF16, False, (9, 5000)),
+             (FP16, True, (600, 24584)), (BF16, True, (530, 151936)), (FP32, True, (3, 128)),
+             (BF16, False, (1300, 16000)), (FP16, True, (1, 777)), (BF16, True, (1025, 4096))]
+    with Dev(hdl) as d:
+        bufs = []
+        for i, (dt, fused, shape) in enumerate(cases):
+            X = logits(dt, shape, seed=300 + i)
+            labels = rng(400 + i).integers(0, shape[1], size=shape[0]).astype(np.uint32)
+            px, pl, po = d.put(X), d.put(labels), d.empty(X.nbytes)
+            ploss, pmean = d.empty(4 * shape[0]), d.empty(4)
+            bufs.append((X, labels, px, pl, po, ploss, pmean))
+        hdl.sync()
+        for rnd in range(2):
+            for (dt, fused, shape), (X, labels, px, pl, po, ploss, pmean) in zip(cases, bufs):
+                if fused:   # in place on px
+                    assert api.submit_softmax_cross_entropy_loss(hdl, 0, dt, shape[0], shape[1], px, pl, ploss, pmean) == 0
+                else:
+                    assert api.submit_softmax(hdl, 0, dt, dt, shape[0], shape[1], px, po) == 0
+            if rnd == 0:
+                hdl.sync()
+                for (dt, fused, shape), (X, labels, px, pl, po, ploss, pmean) in zip(cases, bufs):
+                    if fused:   # the fused op works in place: fresh logits for the next round
+                        hdl.to_device(np.ascontiguousarray(X), px)
+                hdl.sync()
+            else:
+                hdl.sync()
+        for (dt, fused, shape), (X, labels, px, pl, po, ploss, pmean) in zip(cases, bufs):
+            n_rows, n_cols = shape
+            out = d.get(px if fused else po, shape, NP_STORAGE[dt])
+            if fused:
+                lo, hi, loss, mean = np.empty(shape), np.empty(shape), np.empty(n_rows), np.zeros(1)
+                assert oracle().oracle_softmax_cross_entropy(dt, n_rows, n_cols, ptr(X), ptr(labels), ptr(lo), ptr(hi),
+                                                             ptr(loss), ptr(mean)) == 0
+                check_rounded(out, dt, lo, hi, what="fused dlogits %s" % (shape,))
+                check_f32(d.get(ploss, (n_rows,), np.float32), loss, rel=1e-4, what="fused loss %s" % (shape,))
+                check_f32(d.get(pmean, (1,), np.float32), mean, rel=1e-4, what="fused mean loss %s" % (shape,))
+            else:
+                pre = np.empty(shape)
+                assert oracle().oracle_softmax(dt, dt, n_rows, n_cols, ptr(X), ptr(pre)) == 0
+                check_rounded(out, dt, pre, what="softmax %s" % (shape,))
 
 
 def test_softmax_cross_entropy_label_out_of_range(hdl):
