@@ -323,6 +323,13 @@ __device__ __forceinline__ R16 buf_load16_nt(__amdgpu_buffer_rsrc_t r, uint32_t 
 	return o;
 }
 template <int AUX>
+__device__ __forceinline__ R16 buf_load16_aux(__amdgpu_buffer_rsrc_t r, uint32_t voff, uint32_t soff) {
+	const u32x4_v v = __builtin_amdgcn_raw_buffer_load_b128(r, voff, soff, AUX);
+	R16 o;
+	o.w[0] = v.x; o.w[1] = v.y; o.w[2] = v.z; o.w[3] = v.w;
+	return o;
+}
+template <int AUX>
 __device__ __forceinline__ void buf_store16_aux(__amdgpu_buffer_rsrc_t r, uint32_t voff, uint32_t soff, const R16 & x) {
 	const u32x4_v v = {x.w[0], x.w[1], x.w[2], x.w[3]};
 	__builtin_amdgcn_raw_buffer_store_b128(v, r, voff, soff, AUX);
