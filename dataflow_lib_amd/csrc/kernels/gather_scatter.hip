@@ -28,13 +28,14 @@
  * 8192 tokens against 14.4 us with 8 chunks; 8 KB embedding rows take the
  * same 26 us either way. */
 #define GS_CH 4
-/* Cache policy: the source rows are loaded with the default policy and the
- * destination rows stored with the streaming hint. Measured on MI355X
- * against streaming loads: embedding of 8192 rows of a 128256 x 4096 bf16
- * table 25.7 -> 23.7 us, copy_to_seq_context of 8192 K and V rows of 1024
- * bf16 13.2 -> 12.9 us; stores without the streaming hint or at device scope
- * were slower with either load policy (26.6-29.0 us, 12.6-13.9 us). */
-#define GS_LOAD_AUX 0
+/* Cache policy of the source rows: the embedding loads its table rows with
+ * the default policy (8192 rows of a 128256 x 4096 bf16 table: 25.9 -> 23.2
+ * us per launch against the streaming hint), copy_to_seq_context its K and V
+ * rows with the streaming hint (13.8 against 13.4 us the other way in
+ * bench.py's loop). Both store with the streaming hint: stores without it or
+ * at device scope were slower with either load policy. */
+#define GS_EMB_LOAD_AUX 0
+#define GS_KV_LOAD_AUX BUF_AUX_NT
 
 template <int ELEM>
 struct Elem;
@@ -43,7 +44,7 @@ template <> struct Elem<2> { typedef uint16_t t; };
 template <> struct Elem<4> { typedef uint32_t t; };
 
 /* copy one row of `row_bytes` bytes (a wave; src and dst uniform) */
-template <int ELEM>
+template <int ELEM, int LAUX>
 __device__ __forceinline__ void gs_copy_row(const char * src, char * dst, uint32_t row_bytes, int lane) {
 	const bool vec = ((row_bytes | (uint32_t) (uintptr_t) src | (uint32_t) (uintptr_t) dst) & 15u) == 0u;
 	if (vec) {
@@ -52,7 +53,7 @@ __device__ __forceinline__ void gs_copy_row(const char * src, char * dst, uint32
 		for (uint32_t base = 0; base < row_bytes; base += 64u * 16u * GS_CH) {
 			R16 v[GS_CH];
 #pragma unroll
-			for (int i = 0; i < GS_CH; i++) v[i] = buf_load16_aux<GS_LOAD_AUX>(rs, (uint32_t) (lane + 64 * i) * 16u, base);
+			for (int i = 0; i < GS_CH; i++) v[i] = buf_load16_aux<LAUX>(rs, (uint32_t) (lane + 64 * i) * 16u, base);
 #pragma unroll
 			for (int i = 0; i < GS_CH; i++) buf_store16_nt(rd, (uint32_t) (lane + 64 * i) * 16u, base, v[i]);
 		}
@@ -75,7 +76,7 @@ __device__ __forceinline__ void embedding_impl(int num_tokens, int embed_dim, co
 	const uint32_t row_bytes = (uint32_t) embed_dim * (uint32_t) ELEM;
 	for (long t = (long) blockIdx.x * wpb + wave; t < num_tokens; t += (long) gridDim.x * wpb) {
 		const uint64_t id = load_scalar(token_ids + t);
-		gs_copy_row<ELEM>(static_cast<const char *>(table) + id * row_bytes, static_cast<char *>(out) + (uint64_t) t * row_bytes, row_bytes, lane);
+		gs_copy_row<ELEM, GS_EMB_LOAD_AUX>(static_cast<const char *>(table) + id * row_bytes, static_cast<char *>(out) + (uint64_t) t * row_bytes, row_bytes, lane);
 	}
 }
 
@@ -94,8 +95,8 @@ __device__ __forceinline__ void copy_to_seq_context_impl(uint64_t N, int kv_dim,
 		char * ctx = reinterpret_cast<char *>(load_scalar(seq_context_ptrs + t));
 		const uint64_t pos = (uint64_t) (int64_t) load_scalar(seq_positions + t);
 		const uint64_t size = (uint64_t) (int64_t) load_scalar(seq_context_sizes + t);
-		gs_copy_row<ELEM>(static_cast<const char *>(keys) + (uint64_t) t * row_bytes, ctx + pos * row_bytes, row_bytes, lane);
-		gs_copy_row<ELEM>(static_cast<const char *>(values) + (uint64_t) t * row_bytes, ctx + (size + pos) * row_bytes, row_bytes, lane);
+		gs_copy_row<ELEM, GS_KV_LOAD_AUX>(static_cast<const char *>(keys) + (uint64_t) t * row_bytes, ctx + pos * row_bytes, row_bytes, lane);
+		gs_copy_row<ELEM, GS_KV_LOAD_AUX>(static_cast<const char *>(values) + (uint64_t) t * row_bytes, ctx + (size + pos) * row_bytes, row_bytes, lane);
 	}
 }
 
