@@ -370,6 +370,9 @@ static int hip_set_mem(Dataflow_Handle * dataflow_handle, int stream_id, void * 
 		HIP_CHECK_RET(hipSetDevice(dataflow_handle->device_id), -1, "device %d", dataflow_handle->device_id);
 		HIP_CHECK_RET(hipMemset(dev_ptr, val, (size_t) size_bytes), -1, "filling %lu bytes at %p",
 						(unsigned long) size_bytes, dev_ptr);
+		/* hipMemset on device memory may return before the fill is done, and
+		 * the handle's streams do not wait for the null stream */
+		HIP_CHECK_RET(hipStreamSynchronize(0), -1, "filling %lu bytes at %p", (unsigned long) size_bytes, dev_ptr);
 		return 0;
 	}
 	hipStream_t stream;
@@ -424,6 +427,12 @@ static int transfer(Dataflow_Handle * h, int stream_id, void * dst, const void *
 	if (stream_id == -1) {
 		HIP_CHECK_RET(hipSetDevice(h->device_id), -1, "device %d", h->device_id);
 		HIP_CHECK_RET(hipMemcpy(dst, src, (size_t) n, kind), -1, "%s of %lu bytes", what, (unsigned long) n);
+		/* a device-to-device hipMemcpy may return before the copy is done,
+		 * and the handle's streams do not wait for the null stream: finish
+		 * it here, so the transfer is blocking as stream -1 promises */
+		if (kind == hipMemcpyDeviceToDevice) {
+			HIP_CHECK_RET(hipStreamSynchronize(0), -1, "%s of %lu bytes", what, (unsigned long) n);
+		}
 		return 0;
 	}
 	hipStream_t stream;

@@ -52,6 +52,31 @@ def test_transfers_round_trip_on_streams(hdl):
         hdl.free(b)
 
 
+def test_blocking_fill_and_copy_are_done_before_stream_work(hdl):
+    """stream -1 set_mem and device-to-device copies are complete when they
+    return: a copy queued right after them on a (non-blocking) handle stream
+    sees every byte they wrote (256 MiB, long enough that a fill or copy still
+    in flight would be caught)"""
+    n = 256 << 20
+    a, b, c = hdl.alloc(n), hdl.alloc(n), hdl.alloc(n)
+    try:
+        assert hdl.set_mem(c, 0, n) == 0
+        assert hdl.set_mem(a, 0x5A, n) == 0
+        assert hdl.copy(c, a, n, stream_id=1) == 0
+        assert hdl.sync_stream(1) == 0
+        assert (hdl.to_host(c, (n,), np.uint8) == 0x5A).all()
+        assert hdl.set_mem(b, 0, n, stream_id=1) == 0
+        assert hdl.sync_stream(1) == 0
+        assert hdl.set_mem(a, 0xC3, n) == 0
+        assert hdl.copy(b, a, n) == 0   # stream -1: blocking
+        assert hdl.copy(c, b, n, stream_id=1) == 0
+        assert hdl.sync_stream(1) == 0
+        assert (hdl.to_host(c, (n,), np.uint8) == 0xC3).all()
+    finally:
+        for p in (a, b, c):
+            hdl.free(p)
+
+
 def test_dependency_orders_a_copy_after_an_op_on_another_stream(hdl):
     """stream 1 waits for stream 0's state before copying what stream 0's op
     writes, so the copy holds the op's output, not the sentinel before it"""
