@@ -33,6 +33,15 @@
 
 __device__ __forceinline__ float exp_fast(float x) { return __builtin_amdgcn_exp2f(x * SMX_LOG2E); }
 
+/* Factor that moves an online sum of exp(x - ref) from reference `from` to
+ * reference `to` (to >= from once a finite max has been seen). Until then the
+ * reference is a placeholder 0 and the sum is 0: the exponent is clamped at 0
+ * so that moving it to a max below -88 multiplies 0 by 1, not by an
+ * overflowed exp (0 * inf would make the sum NaN). */
+__device__ __forceinline__ float online_rescale(float from, float to) {
+	return __builtin_amdgcn_exp2f(fminf((from - to) * SMX_LOG2E, 0.0f));
+}
+
 template <typename T> __device__ __forceinline__ float rnd_in(float f) { return to_f(from_f<T>(f)); }
 
 /* Block reductions: each wave's partial goes to its LDS cell, one barrier,
@@ -414,17 +423,16 @@ __device__ __forceinline__ void smx_regs(int n_rows, int n_cols, const T * X, TO
 				}
 				if (SX) {
 					const float mr = (cm == -__builtin_inff()) ? 0.0f : cm;
-					so *= __builtin_amdgcn_exp2f((mref - mr) * SMX_LOG2E);
-					const float nb = -mr * SMX_LOG2E;
+					so *= online_rescale(mref, mr);
 #pragma unroll
-					for (int e = 0; e < VEC; e++) so += __builtin_amdgcn_exp2f(fmaf(f[e], SMX_LOG2E, nb));
+					for (int e = 0; e < VEC; e++) so += __builtin_amdgcn_exp2f((f[e] - mr) * SMX_LOG2E);
 					mref = mr;
 				}
 				m = cm;
 			}
 		}
 		m = cells_max(m, mslots);
-		if (SX) so *= __builtin_amdgcn_exp2f((mref - m) * SMX_LOG2E);   /* sx against the row max */
+		if (SX) so *= online_rescale(mref, m);   /* sx against the row max */
 #pragma unroll
 		for (int c = 0; c < SMX_MAXCH; c++) reg_barrier(xr[c]);
 
@@ -501,7 +509,7 @@ __device__ __forceinline__ void smx_regs(int n_rows, int n_cols, const T * X, TO
 		 * arrived. */
 		static_assert(SMX_MAXCH == 16, "the wait below counts SMX_MAXCH stores");
 		__builtin_amdgcn_s_waitcnt(0x4F70);   /* vmcnt(16); expcnt, lgkmcnt at their maxima */
-		if (FUSED && tid == 0 && loss) store_loss(loss, row, lab_ok ? (logf(sx) + m - xlab_cell[par]) : __builtin_nanf(""));
+		if (FUSED && tid == 0 && loss) store_loss(loss, row, lab_ok ? (logf(sx) + (m - xlab_cell[par])) : __builtin_nanf(""));
 		par ^= 1;
 		row = next;
 		next = next2;
@@ -542,7 +550,7 @@ __device__ __forceinline__ void smx_stream(int n_rows, int n_cols, const T * X, 
 			orow[j] = from_f<TO>(y);
 		}
 		if (FUSED && tid == 0 && loss) {
-			store_loss(loss, row, (lab < (uint32_t) n_cols) ? (logf(sx) + m - x_lab) : __builtin_nanf(""));
+			store_loss(loss, row, (lab < (uint32_t) n_cols) ? (logf(sx) + (m - x_lab)) : __builtin_nanf(""));
 		}
 		__syncthreads();
 	}
@@ -600,7 +608,7 @@ __device__ __forceinline__ void smx_stream_vec(int n_rows, int n_cols, const T *
 				if (c == c_lab) xlab_cell = f[k][le];
 			}
 			const float mr = (cm == -__builtin_inff()) ? 0.0f : cm;
-			s *= __builtin_amdgcn_exp2f((mref - mr) * SMX_LOG2E);
+			s *= online_rescale(mref, mr);
 #pragma unroll
 			for (int k = 0; k < U; k++) {
 #pragma unroll
@@ -610,7 +618,7 @@ __device__ __forceinline__ void smx_stream_vec(int n_rows, int n_cols, const T *
 			m = cm;
 		}
 		const float mx = block_max(m, slots);
-		float sx = s * __builtin_amdgcn_exp2f((mref - mx) * SMX_LOG2E);
+		float sx = s * online_rescale(mref, mx);
 		/* pass 2 (fp16/bf16): sd = sum exp(rnd(x - mx)) */
 		float sd = 0.0f;
 		if (ROUNDS) {
@@ -654,7 +662,7 @@ __device__ __forceinline__ void smx_stream_vec(int n_rows, int n_cols, const T *
 				buf_store16_nt(rout, (uint32_t) c * 16u, 0, o);
 			}
 		}
-		if (FUSED && tid == 0 && loss) store_loss(loss, row, lab_ok ? (logf(sx) + mx - xlab_cell) : __builtin_nanf(""));
+		if (FUSED && tid == 0 && loss) store_loss(loss, row, lab_ok ? (logf(sx) + (mx - xlab_cell)) : __builtin_nanf(""));
 		__syncthreads();   /* the cells are rewritten for the next row */
 	}
 }

@@ -762,6 +762,64 @@ def test_fused_loss_on_confident_rows(hdl):
     check_f32(gm, mean, rel=1e-4, what="fused mean loss, confident rows")
 
 
+def shifted_logits(dt, shape, seed):
+    """Rows moved far from 0: all values near -200 or -10000 (below the
+    range where exp of the max is representable against a reference of 0),
+    near -150 behind a -inf prefix that fills every lane's first chunks,
+    near +10000 (where the loss is a small number next to the max), and two
+    ordinary rows."""
+    n_rows, n_cols = shape
+    x = normal(seed, shape, std=2.0)
+    shifts = [-200.0, -150.0, 1.0e4, -1.0e4, 60.0, 0.0]
+    for r in range(n_rows):
+        x[r] += shifts[r % len(shifts)]
+    x[1, : min(32768, n_cols // 2)] = -np.inf
+    return to_storage(x, dt)
+
+
+SHIFTED_SHAPES = [(6, 128256), (6, 151936), (6, 1001)]   # register path (16-bit), streaming vector path, element path
+
+
+@pytest.mark.parametrize("dt", DTS, ids=dt_id)
+@pytest.mark.parametrize("shape", SHIFTED_SHAPES, ids=lambda s: "%dx%d" % s)
+def test_fused_loss_on_shifted_rows(hdl, dt, shape):
+    from dataflow_lib_amd import api
+    n_rows, n_cols = shape
+    X = shifted_logits(dt, shape, seed=731)
+    labels = rng(732).integers(0, n_cols, size=n_rows).astype(np.uint32)
+    labels[1] = n_cols - 1
+    lo, hi, loss, mean = np.empty(shape), np.empty(shape), np.empty(n_rows), np.zeros(1)
+    assert oracle().oracle_softmax_cross_entropy(dt, n_rows, n_cols, ptr(X), ptr(labels), ptr(lo), ptr(hi),
+                                                 ptr(loss), ptr(mean)) == 0
+    assert np.isfinite(loss).all()
+    with Dev(hdl) as d:
+        px, pl, ploss, pmean = d.put(X), d.put(labels), d.empty(4 * n_rows), d.empty(4)
+        assert api.submit_softmax_cross_entropy_loss(hdl, 0, dt, n_rows, n_cols, px, pl, ploss, pmean) == 0
+        out = d.get(px, shape, NP_STORAGE[dt])
+        gl = d.get(ploss, (n_rows,), np.float32)
+        gm = d.get(pmean, (1,), np.float32)
+    check_rounded(out, dt, lo, hi, what="fused dlogits, shifted rows")
+    check_f32(gl, loss, rel=1e-4, what="fused loss, shifted rows")
+    check_f32(gm, mean, rel=1e-4, what="fused mean loss, shifted rows")
+
+
+@pytest.mark.parametrize("dt", DTS, ids=dt_id)
+@pytest.mark.parametrize("shape", SHIFTED_SHAPES, ids=lambda s: "%dx%d" % s)
+def test_softmax_on_shifted_rows(hdl, dt, shape):
+    """fp32 rows past the register path take their softmax sum from the
+    online pass, so the shifted rows reach the softmax itself there"""
+    from dataflow_lib_amd import api
+    n_rows, n_cols = shape
+    X = shifted_logits(dt, shape, seed=741)
+    pre = np.empty(shape)
+    assert oracle().oracle_softmax(dt, dt, n_rows, n_cols, ptr(X), ptr(pre)) == 0
+    with Dev(hdl) as d:
+        px, po = d.put(X), d.empty(X.nbytes)
+        assert api.submit_softmax(hdl, 0, dt, dt, n_rows, n_cols, px, po) == 0
+        out = d.get(po, shape, NP_STORAGE[dt])
+    check_rounded(out, dt, pre, what="softmax, shifted rows")
+
+
 def test_softmax_row_counter_across_launches(hdl):
     """The 16-bit and fp32 softmax kernels hand rows past each workgroup's
     first two out from a counter in the code object, and the last workgroup
