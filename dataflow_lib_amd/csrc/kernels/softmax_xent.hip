@@ -394,14 +394,16 @@ __device__ __forceinline__ void smx_regs(int n_rows, int n_cols, const T * X, TO
 		 * passes). Each request sits just before this row's chunk c is used
 		 * (the scheduling barrier keeps that order), so the waves compute
 		 * while the memory pipeline accepts them. For the loss, sx is summed
-		 * in the same pass online: so = sum exp(x - mref) against the running
-		 * max (mref = 0 while that is still -inf), rescaled when the max
-		 * grows. (Summing it in the sum pass instead, from exp(d) corrected
+		 * in the same pass online: so = sum exp(x - mref) against a reference
+		 * that trails the running max by at most 64, rescaled when it moves.
+		 * (Summing it in the sum pass instead, from exp(d) corrected
 		 * for the rounding of x - m, measured 7 us faster to first order but
 		 * misses the 1e-4 loss bound on confident rows, and 28 us slower to
 		 * second order: that pass is already the kernel's busiest.) */
 		float m = -__builtin_inff();
-		float mref = 0.0f, so = 0.0f;
+		/* mref: the online sum's reference, a placeholder 0 until the lane
+		 * has seen a finite value; mref64 = mref + 64, -inf until then */
+		float mref = 0.0f, mref64 = -__builtin_inff(), so = 0.0f;
 #pragma unroll
 		for (int c = 0; c < SMX_MAXCH; c++) {
 			if (c >= SMX_PF) issue_next(c);
@@ -422,11 +424,19 @@ __device__ __forceinline__ void smx_regs(int n_rows, int n_cols, const T * X, TO
 					xlab_cell[par] = xl;
 				}
 				if (SX) {
-					const float mr = (cm == -__builtin_inff()) ? 0.0f : cm;
-					so *= online_rescale(mref, mr);
+					/* the reference moves only when this lane's max passes it
+					 * by more than 64 (rare after the first chunk: a
+					 * wave-uniform branch), so the terms stay below e^64 and
+					 * 128 of them cannot overflow; measured 382.2 -> 380.8 us
+					 * against moving it every chunk */
+					const bool move = cm > mref64;
+					if (__builtin_amdgcn_ballot_w64(move)) {
+						so = move ? so * online_rescale(mref, cm) : so;
+						mref = move ? cm : mref;
+						mref64 = move ? cm + 64.0f : mref64;
+					}
 #pragma unroll
-					for (int e = 0; e < VEC; e++) so += __builtin_amdgcn_exp2f((f[e] - mr) * SMX_LOG2E);
-					mref = mr;
+					for (int e = 0; e < VEC; e++) so += __builtin_amdgcn_exp2f((f[e] - mref) * SMX_LOG2E);
 				}
 				m = cm;
 			}
