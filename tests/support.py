@@ -92,6 +92,17 @@ def to_storage(x32, dt):
     return f32_to_bf16_bits(x32)
 
 
+def rope_pair_floor(x, width):
+    """fp32 evaluation floor of a rotated pair, per output element: the two
+    products of each output are at most |e| + |o| (|cos|, |sin| <= 1), and
+    the fp32 tables and products carry a few 2^-24 of that, which remains
+    when the products cancel: 8 * 2^-24 * (|e| + |o|), for both outputs of
+    the pair. x holds the input rows as floats, `width` columns each."""
+    v = np.abs(np.asarray(x, dtype=np.float64).reshape(-1, width))
+    m = v[:, 0::2] + v[:, 1::2]
+    return np.repeat(m, 2, axis=1).ravel() * 8.0 * 2.0 ** -24
+
+
 def to_f64(a, dt):
     if dt in FP8_MAX:
         a = np.ascontiguousarray(a, dtype=np.uint8)

@@ -14,7 +14,7 @@ import numpy as np
 import pytest
 
 from support import (BF16, FP16, FP8_MAX, FP8E4M3, FP8E5M2, NP_STORAGE, check_f32, check_rounded, gamma, normal, oracle,
-                     ptr, rms_dw_fp8_depth, rms_ws_depth, rng, to_f64, to_storage)
+                     ptr, rms_dw_fp8_depth, rms_ws_depth, rng, rope_pair_floor, to_f64, to_storage)
 from test_hip_ops import Dev, hdl  # noqa: F401  (the module's handle fixture)
 
 pytestmark = pytest.mark.gpu
@@ -233,6 +233,33 @@ def test_rope_fp8(hdl, dt, case):
     check_rounded(gq, dt, qv, what="rope fp8 Q")
     if K.size:
         check_rounded(gk, dt, kv, what="rope fp8 K")
+
+
+ROPE_F8_LARGE_STD = {FP8E4M3: 100.0, FP8E5M2: 1.0e4}
+
+
+@pytest.mark.parametrize("dt", F8, ids=dt_id)
+def test_rope_fp8_large_magnitudes(hdl, dt):
+    """fp8 inputs spread over the format's range (E4M3 up to its 448
+    saturation, E5M2 std 1e4): the plain fp32 rotation the fp8 kernels use
+    stays within one fp8 ulp of the exact result, plus the fp32 evaluation
+    floor (rope_pair_floor) where the two products cancel, which in E5M2's
+    subnormal range is wider than an ulp"""
+    from dataflow_lib_amd import api
+    T, nq, nkv, hd, theta = 256, 32, 8, 128, 500000
+    Q = to_storage(normal(771, (T, nq * hd), std=ROPE_F8_LARGE_STD[dt]), dt)
+    K = to_storage(normal(772, (T, nkv * hd), std=ROPE_F8_LARGE_STD[dt]), dt)
+    pos = rng(773).integers(0, 131072, size=T).astype(np.int32)
+    N = T * nq * hd
+    qv, kv = np.empty(Q.shape), np.empty(K.shape)
+    assert oracle().oracle_rope(dt, 0, N, nq * hd, hd, nkv, theta, ptr(pos), ptr(Q), ptr(K), ptr(qv), ptr(kv)) == 0
+    with Dev(hdl) as d:
+        pq, pk, pp = d.put(Q), d.put(K), d.put(pos)
+        assert api.submit_rope(hdl, 0, dt, N, nq * hd, hd, nkv, theta, pp, pq, pk) == 0
+        gq = d.get(pq, Q.shape, np.uint8)
+        gk = d.get(pk, K.shape, np.uint8)
+    check_rounded(gq, dt, qv, floor=rope_pair_floor(to_f64(Q, dt), nq * hd), what="rope fp8 Q, large magnitudes")
+    check_rounded(gk, dt, kv, floor=rope_pair_floor(to_f64(K, dt), nkv * hd), what="rope fp8 K, large magnitudes")
 
 
 def test_rope_bwd_has_no_fp8_variant(hdl):

@@ -16,7 +16,7 @@ import numpy as np
 import pytest
 
 from support import (BF16, FP16, FP32, NP_STORAGE, check_f32, check_rounded, confident_logits, gamma, normal, oracle, ptr,
-                     rms_dw_depth, rms_ws_depth, rng, sum_gate, to_f64, to_storage)
+                     rms_dw_depth, rms_ws_depth, rng, rope_pair_floor, sum_gate, to_f64, to_storage)
 
 pytestmark = pytest.mark.gpu
 DTS = [FP32, FP16, BF16]
@@ -417,6 +417,35 @@ def test_rope(hdl, dt, case, bwd):
     check_rounded(gq, dt, qv, what="rope Q")
     if K.size:
         check_rounded(gk, dt, kv, what="rope K")
+
+
+ROPE_LARGE_STD = {FP32: 1.0e6, FP16: 8.0e3, BF16: 1.0e4}
+
+
+@pytest.mark.parametrize("bwd", [0, 1], ids=["fwd", "bwd"])
+@pytest.mark.parametrize("dt", DTS, ids=dt_id)
+def test_rope_large_magnitudes(hdl, dt, bwd):
+    """Inputs far from unit scale (std 1e4; fp16 8e3, fp32 1e6). Where a
+    pair's two products cancel, the exact result is small next to them and
+    even correctly rounded fp32 cos/sin tables leave an error of a few 2^-24
+    of the products, so the tolerance adds that floor (rope_pair_floor) to
+    the output type's ulp; elsewhere the ulp alone decides."""
+    from dataflow_lib_amd import api
+    T, nq, nkv, hd, theta = 256, 32, 8, 128, 500000
+    Q = to_storage(normal(761, (T, nq * hd), std=ROPE_LARGE_STD[dt]), dt)
+    K = to_storage(normal(762, (T, nkv * hd), std=ROPE_LARGE_STD[dt]), dt)
+    pos = rng(763).integers(0, 131072, size=T).astype(np.int32)
+    N = T * nq * hd
+    qv, kv = np.empty(Q.shape), np.empty(K.shape)
+    assert oracle().oracle_rope(dt, bwd, N, nq * hd, hd, nkv, theta, ptr(pos), ptr(Q), ptr(K), ptr(qv), ptr(kv)) == 0
+    with Dev(hdl) as d:
+        pq, pk, pp = d.put(Q), d.put(K), d.put(pos)
+        fn = api.submit_rope_bwd_x if bwd else api.submit_rope
+        assert fn(hdl, 0, dt, N, nq * hd, hd, nkv, theta, pp, pq, pk) == 0
+        gq = d.get(pq, Q.shape, NP_STORAGE[dt])
+        gk = d.get(pk, K.shape, NP_STORAGE[dt])
+    check_rounded(gq, dt, qv, floor=rope_pair_floor(to_f64(Q, dt), nq * hd), what="rope Q, large magnitudes")
+    check_rounded(gk, dt, kv, floor=rope_pair_floor(to_f64(K, dt), nkv * hd), what="rope K, large magnitudes")
 
 
 @pytest.mark.parametrize("theta", [10000, 500000])
