@@ -374,7 +374,7 @@ PREROLL = 3
 SETTLE_STEPS = 10
 
 
-def time_ops(h, hip, ops, steps, warmup, batches=5):
+def time_ops(h, hip, ops, steps, warmup, batches=20):
     """Time `steps` steps (each op once per step, rotating buffer sets) on one
     stream, with events only at the two ends (an event recorded between
     kernels costs the stream several microseconds, which would be counted as
