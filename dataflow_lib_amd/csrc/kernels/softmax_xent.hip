@@ -42,6 +42,20 @@ __device__ __forceinline__ float online_rescale(float from, float to) {
 	return __builtin_amdgcn_exp2f(fminf((from - to) * SMX_LOG2E, 0.0f));
 }
 
+/* The fused loss -log p_label = log(sum_j exp(x_j - m)) + m - x_label, from
+ * `others` = the sum of exp(x_j - m) over every column but the label's, the
+ * row max m and the labelled logit xl. While the label is within 16 of the
+ * max it is log1p(others / exp(xl - m)): a row the label wins by far has a
+ * loss of about `others`, which log(1 + others) in fp32 would round away
+ * below 2^-24 (and lose relative precision well above that). Further down,
+ * log(others + exp(xl - m)) + (m - xl); NaN and infinite inputs take that
+ * form too. */
+__device__ __forceinline__ float fused_loss(float others, float m, float xl) {
+	const float gap = m - xl;
+	const float el = __builtin_amdgcn_exp2f(-gap * SMX_LOG2E);
+	return (gap < 16.0f) ? log1pf(others / el) : (logf(others + el) + gap);
+}
+
 template <typename T> __device__ __forceinline__ float rnd_in(float f) { return to_f(from_f<T>(f)); }
 
 /* Block reductions: each wave's partial goes to its LDS cell, one barrier,
@@ -267,10 +281,10 @@ __device__ __forceinline__ void smx_regs(int n_rows, int n_cols, const T * X, TO
 	using W = SmxWord<T>;
 	using WO = SmxWord<TO>;
 	static_assert(sizeof(T) == sizeof(TO), "in-register output packing needs equal widths");
-	/* the loss needs sx = sum exp(x - m) over the unrounded differences; with
-	 * 16-bit storage that is not sum exp(d), so it is accumulated separately
-	 * (fp32 differences are not rounded: sx = sd) */
-	constexpr bool SX = FUSED && sizeof(T) < 4;
+	/* the loss needs sx = sum exp(x - m) over the unrounded differences and
+	 * without the label's column (fused_loss); that is not the softmax's sum,
+	 * so it is accumulated separately, for every storage type */
+	constexpr bool SX = FUSED;
 	/* separate LDS cells for the max and the sum: each is rewritten only after
 	 * every wave has passed the other reduction's barrier, so reuse needs no
 	 * barrier of its own (two barriers per row) */
@@ -422,6 +436,11 @@ __device__ __forceinline__ void smx_regs(int n_rows, int n_cols, const T * X, TO
 					for (int e = 1; e < VEC; e++)
 						if (e == le) xl = f[e];
 					xlab_cell[par] = xl;
+					/* the loss sum leaves the label's column out (the max
+					 * above already has it) */
+#pragma unroll
+					for (int e = 0; e < VEC; e++)
+						if (e == le) f[e] = -__builtin_inff();
 				}
 				if (SX) {
 					/* the reference moves only when this lane's max passes it
@@ -519,7 +538,7 @@ __device__ __forceinline__ void smx_regs(int n_rows, int n_cols, const T * X, TO
 		 * arrived. */
 		static_assert(SMX_MAXCH == 16, "the wait below counts SMX_MAXCH stores");
 		__builtin_amdgcn_s_waitcnt(0x4F70);   /* vmcnt(16); expcnt, lgkmcnt at their maxima */
-		if (FUSED && tid == 0 && loss) store_loss(loss, row, lab_ok ? (logf(sx) + (m - xlab_cell[par])) : __builtin_nanf(""));
+		if (FUSED && tid == 0 && loss) store_loss(loss, row, lab_ok ? fused_loss(sx, m, xlab_cell[par]) : __builtin_nanf(""));
 		par ^= 1;
 		row = next;
 		next = next2;
@@ -549,7 +568,7 @@ __device__ __forceinline__ void smx_stream(int n_rows, int n_cols, const T * X, 
 		for (int j = tid; j < n_cols; j += nt) {
 			const float diff = to_f(xrow[j]) - m;
 			sd += exp_fast(rnd_in<T>(diff));
-			if (FUSED) sx += exp_fast(diff);
+			if (FUSED && (uint32_t) j != lab) sx += exp_fast(diff);
 		}
 		__syncthreads();
 		block_sum2(sd, sx, slots);
@@ -560,7 +579,7 @@ __device__ __forceinline__ void smx_stream(int n_rows, int n_cols, const T * X, 
 			orow[j] = from_f<TO>(y);
 		}
 		if (FUSED && tid == 0 && loss) {
-			store_loss(loss, row, (lab < (uint32_t) n_cols) ? (logf(sx) + (m - x_lab)) : __builtin_nanf(""));
+			store_loss(loss, row, (lab < (uint32_t) n_cols) ? fused_loss(sx, m, x_lab) : __builtin_nanf(""));
 		}
 		__syncthreads();
 	}
@@ -606,6 +625,9 @@ __device__ __forceinline__ void smx_stream_vec(int n_rows, int n_cols, const T *
 			for (int k = 0; k < U; k++) v[k] = buf_load16(rin, (uint32_t) (base + k * nt + tid) * 16u, 0);
 			float f[U][VEC];
 			float cm = m;
+			/* the element of each chunk that the loss sum leaves out: the
+			 * label's (the max has it), or none (-1) */
+			int skip[U];
 #pragma unroll
 			for (int k = 0; k < U; k++) {
 				const int c = base + k * nt + tid;
@@ -616,13 +638,17 @@ __device__ __forceinline__ void smx_stream_vec(int n_rows, int n_cols, const T *
 					cm = fmaxf(cm, f[k][e]);
 				}
 				if (c == c_lab) xlab_cell = f[k][le];
+				skip[k] = (c == c_lab) ? le : -1;
 			}
 			const float mr = (cm == -__builtin_inff()) ? 0.0f : cm;
 			s *= online_rescale(mref, mr);
 #pragma unroll
 			for (int k = 0; k < U; k++) {
 #pragma unroll
-				for (int e = 0; e < VEC; e++) s += __builtin_amdgcn_exp2f((f[k][e] - mr) * SMX_LOG2E);
+				for (int e = 0; e < VEC; e++) {
+					const float term = __builtin_amdgcn_exp2f((f[k][e] - mr) * SMX_LOG2E);
+					s += (e == skip[k]) ? 0.0f : term;
+				}
 			}
 			mref = mr;
 			m = cm;
@@ -649,7 +675,8 @@ __device__ __forceinline__ void smx_stream_vec(int n_rows, int n_cols, const T *
 		}
 		__syncthreads();   /* every wave has read the max cells */
 		block_sum2(sx, sd, slots);
-		if (!ROUNDS) sd = sx;
+		/* fp32: the softmax's sum is the loss sum plus the label's term */
+		if (!ROUNDS) sd = sx + (lab_ok ? __builtin_amdgcn_exp2f((xlab_cell - mx) * SMX_LOG2E) : 0.0f);
 		const float nlog2s = -__builtin_amdgcn_logf(sd);
 		/* last pass: y = exp(rnd(x - mx)) / sd */
 		for (int base = 0; base < nv; base += nt * U) {
@@ -672,7 +699,7 @@ __device__ __forceinline__ void smx_stream_vec(int n_rows, int n_cols, const T *
 				buf_store16_nt(rout, (uint32_t) c * 16u, 0, o);
 			}
 		}
-		if (FUSED && tid == 0 && loss) store_loss(loss, row, lab_ok ? (logf(sx) + (mx - xlab_cell)) : __builtin_nanf(""));
+		if (FUSED && tid == 0 && loss) store_loss(loss, row, lab_ok ? fused_loss(sx, mx, xlab_cell) : __builtin_nanf(""));
 		__syncthreads();   /* the cells are rewritten for the next row */
 	}
 }

@@ -172,7 +172,15 @@ void cpu_ref_softmax_xent_bf16(int n_rows, int n_cols, uint16_t * logits, const 
 			#pragma omp simd
 			for (int j = 0; j < n_cols; j++) x[j] = to_bf(e[j] * inv);
 			if (lab < (uint32_t) n_cols) x[lab] = to_bf(bf(x[lab]) - 1.0f);
-			loss[r] = lab < (uint32_t) n_cols ? (float) log(s) + m - xl : NAN;
+			if (lab < (uint32_t) n_cols) {
+				/* -log p_label = log1p(others / exp(x_l - m)), as the kernels
+				 * form it, with others = s less the label's term */
+				const double gap = (double) m - (double) xl, others = s - (double) e[lab];
+				loss[r] = (float) (gap < 16.0 ? log1p(others / exp(-gap)) : log(others + exp(-gap)) + gap);
+			}
+			else {
+				loss[r] = NAN;
+			}
 			total += loss[r];
 		}
 		free(e);

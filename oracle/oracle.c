@@ -515,7 +515,17 @@ static int softmax_xent_impl(int dt, int n_rows, int n_cols, const void * X, con
 			const double hi = oracle_round(p * (1.0 + slack), dt) - 1.0;
 			y_lo[base + lab] = lo;
 			if (y_hi) y_hi[base + lab] = hi;
-			if (loss) loss[r] = log(sx) + m - load1(dt, X, base + lab);
+			if (loss) {
+				/* -log p_label = log1p(others / exp(x_l - m)), others = the sum
+				 * of exp(x_j - m) over the other columns: log(sx) + m - x_l
+				 * loses a confident row's small loss in fp64 too (below
+				 * ~1e-12); the same form as the kernels, evaluated in fp64 */
+				const double xl = load1(dt, X, base + lab), gap = m - xl;
+				double others = 0.0;
+				for (int j = 0; j < n_cols; j++)
+					if ((uint32_t) j != lab) others += exp(load1(dt, X, base + j) - m);
+				loss[r] = (gap < 16.0) ? log1p(others / exp(-gap)) : log(others + exp(-gap)) + gap;
+			}
 		}
 		else if (loss) {
 			loss[r] = NAN;

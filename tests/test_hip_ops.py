@@ -834,6 +834,36 @@ def test_fused_loss_on_shifted_rows(hdl, dt, shape):
 
 @pytest.mark.parametrize("dt", DTS, ids=dt_id)
 @pytest.mark.parametrize("shape", SHIFTED_SHAPES, ids=lambda s: "%dx%d" % s)
+def test_fused_loss_keeps_small_losses(hdl, dt, shape):
+    """Rows the label wins by 5 to 40 over a N(0, 1) bulk, so each loss is
+    about the sum of the other columns' exp(x - x_label): from ~1e-1 down
+    to ~1e-12. The 1e-4 relative bound then needs the loss formed from that
+    sum (log1p of it) rather than from log(1 + sum) in fp32, which rounds a
+    loss below 2^-24 to 0 and loses relative precision well above that."""
+    from dataflow_lib_amd import api
+    n_rows, n_cols = shape
+    x = normal(781, shape)
+    labels = rng(782).integers(0, n_cols, size=n_rows).astype(np.uint32)
+    for r in range(n_rows):
+        x[r, labels[r]] = 5.0 + 7.0 * r
+    X = to_storage(x, dt)
+    lo, hi, loss, mean = np.empty(shape), np.empty(shape), np.empty(n_rows), np.zeros(1)
+    assert oracle().oracle_softmax_cross_entropy(dt, n_rows, n_cols, ptr(X), ptr(labels), ptr(lo), ptr(hi),
+                                                 ptr(loss), ptr(mean)) == 0
+    assert loss.min() < 1e-9 and loss.max() > 1e-3
+    with Dev(hdl) as d:
+        px, pl, ploss, pmean = d.put(X), d.put(labels), d.empty(4 * n_rows), d.empty(4)
+        assert api.submit_softmax_cross_entropy_loss(hdl, 0, dt, n_rows, n_cols, px, pl, ploss, pmean) == 0
+        out = d.get(px, shape, NP_STORAGE[dt])
+        gl = d.get(ploss, (n_rows,), np.float32)
+        gm = d.get(pmean, (1,), np.float32)
+    check_rounded(out, dt, lo, hi, what="fused dlogits, small losses")
+    check_f32(gl, loss, rel=1e-4, what="fused loss, small losses")
+    check_f32(gm, mean, rel=1e-4, what="fused mean loss, small losses")
+
+
+@pytest.mark.parametrize("dt", DTS, ids=dt_id)
+@pytest.mark.parametrize("shape", SHIFTED_SHAPES, ids=lambda s: "%dx%d" % s)
 def test_softmax_on_shifted_rows(hdl, dt, shape):
     """fp32 rows past the register path take their softmax sum from the
     online pass, so the shifted rows reach the softmax itself there"""
