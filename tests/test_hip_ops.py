@@ -862,6 +862,44 @@ def test_fused_loss_keeps_small_losses(hdl, dt, shape):
     check_f32(gm, mean, rel=1e-4, what="fused mean loss, small losses")
 
 
+MARGIN_SHAPES = [(96, 128256), (96, 151936), (96, 1001)]   # register path (16-bit), streaming vector path, element path
+
+
+@pytest.mark.parametrize("dt", DTS, ids=dt_id)
+@pytest.mark.parametrize("shape", MARGIN_SHAPES, ids=lambda s: "%dx%d" % s)
+def test_fused_loss_across_label_margins(hdl, dt, shape):
+    """The label's logit set from 24 below to 40 above the rest of its row
+    (N(0, 1)), in 96 even steps, so that the kernel's loss takes each of its
+    three forms: log(others + exp(x_label - m)) + (m - x_label) once the label
+    trails the max by 16 or more; log1p(y), y = others * exp(m - x_label), from
+    the hardware log with the rounding of 1 + y cancelled while y >= 1/32; and
+    a Taylor polynomial below that (losses down to ~1e-14). Gated at 1e-5
+    relative, ten times tighter than the parity bound: a wrong or dropped term
+    in any form moves some loss well past it, while fp32 summation of up to
+    151936 terms stays below it."""
+    from dataflow_lib_amd import api
+    n_rows, n_cols = shape
+    x = normal(791, shape)
+    labels = ((np.arange(n_rows) * 7919 + 13) % n_cols).astype(np.uint32)
+    margins = np.linspace(-24.0, 40.0, n_rows)
+    for r in range(n_rows):
+        x[r, labels[r]] = np.delete(x[r], labels[r]).max() + margins[r]
+    X = to_storage(x, dt)
+    lo, hi, loss, mean = np.empty(shape), np.empty(shape), np.empty(n_rows), np.zeros(1)
+    assert oracle().oracle_softmax_cross_entropy(dt, n_rows, n_cols, ptr(X), ptr(labels), ptr(lo), ptr(hi),
+                                                 ptr(loss), ptr(mean)) == 0
+    assert loss.min() < 1e-9 and loss.max() > 16.0
+    with Dev(hdl) as d:
+        px, pl, ploss, pmean = d.put(X), d.put(labels), d.empty(4 * n_rows), d.empty(4)
+        assert api.submit_softmax_cross_entropy_loss(hdl, 0, dt, n_rows, n_cols, px, pl, ploss, pmean) == 0
+        out = d.get(px, shape, NP_STORAGE[dt])
+        gl = d.get(ploss, (n_rows,), np.float32)
+        gm = d.get(pmean, (1,), np.float32)
+    check_rounded(out, dt, lo, hi, what="fused dlogits, label margins")
+    check_f32(gl, loss, rel=1e-5, what="fused loss, label margins")
+    check_f32(gm, mean, rel=1e-5, what="fused mean loss, label margins")
+
+
 @pytest.mark.parametrize("dt", DTS, ids=dt_id)
 @pytest.mark.parametrize("shape", SHIFTED_SHAPES, ids=lambda s: "%dx%d" % s)
 def test_softmax_on_shifted_rows(hdl, dt, shape):
