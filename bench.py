@@ -30,7 +30,10 @@ cross_entropy_loss) and the path's neighbours (embedding gather of 8192 rows
 of a 128256 x 4096 bf16 table; copy_to_seq_context of K, V [8192 x 1024] bf16
 into 4 contexts of 2048 positions; rope_copy_to_seq_context, RoPE fused with
 that scatter, on the config-3 Q, K and those contexts) and the fp8 variants
-at the same shapes (E4M3 forward tensors, bf16 backward ones). `transformer_head`:
+at the same shapes (E4M3 forward tensors, bf16 backward ones). `storage_types`:
+the step again with fp16 and with fp32 storage at the same shapes (each
+op's bytes scaled by its element size), its own step time and per-op
+times. `transformer_head`:
 the loss-path driver
 (submit_transformer_head, training pass) at 4096 tokens x 4096 x 128256, whose
 time is its three hipBLASLt GEMMs (reported in TFLOP/s).
@@ -59,7 +62,10 @@ sys.path.insert(0, ROOT)
 HBM_PEAK_GBPS = 8000.0
 GiB = 1 << 30
 BF16 = 5
+FP16 = 4
 FP32 = 3
+ELEM_BYTES = {BF16: 2, FP16: 2, FP32: 4}
+NORMAL_FILL = {BF16: "normal_bf16", FP16: "normal_fp16", FP32: "normal_fp32"}
 
 
 class Hip:
@@ -140,6 +146,10 @@ class Pool:
             g = np.random.default_rng(seed)
             if kind == "normal_bf16":
                 host = bf16_bits(a + b * g.standard_normal(self.block_elems, dtype=np.float32))
+            elif kind == "normal_fp16":
+                host = (a + b * g.standard_normal(self.block_elems, dtype=np.float32)).astype(np.float16)
+            elif kind == "normal_fp32":
+                host = a + b * g.standard_normal(self.block_elems, dtype=np.float32)
             elif kind == "normal_fp8e4m3":
                 host = fp8e4m3_bits(a + b * g.standard_normal(self.block_elems, dtype=np.float32))
             elif kind == "zeros":
@@ -187,70 +197,72 @@ def n_sets(set_bytes):
     return max(1, -(-GiB // set_bytes))
 
 
-def build_ops(h, pool, api):
-    """(name, algorithmic bytes per launch, list of per-set callables)"""
+def build_ops(h, pool, api, dt=BF16):
+    """(name, algorithmic bytes per launch, list of per-set callables); `dt`
+    is the storage type of every tensor but the fp32 statistics and dW"""
+    es, fill = ELEM_BYTES[dt], NORMAL_FILL[dt]
     ops = []
     T, D = 8192, 4096
-    act = T * D * 2
+    act = T * D * es
     # --- RMSNorm fwd: read X, W; write Y, weighted_sums, rstd
-    b_fwd = 2 * act + D * 2 + 2 * T * 4
+    b_fwd = 2 * act + D * es + 2 * T * 4
     runs = []
     for s in range(n_sets(2 * act)):
-        X = pool.fill(act, "normal_bf16", 1)
-        W = pool.fill(D * 2, "normal_bf16", 2, 1.0, 0.02)
+        X = pool.fill(act, fill, 1)
+        W = pool.fill(D * es, fill, 2, 1.0, 0.02)
         Y, ws, rs = pool.empty(act), pool.empty(T * 4), pool.empty(T * 4)
-        runs.append(lambda X=X, W=W, Y=Y, ws=ws, rs=rs: api.submit_rms_norm(h, 0, BF16, T, D, 1e-5, W, X, Y, ws, rs))
+        runs.append(lambda X=X, W=W, Y=Y, ws=ws, rs=rs: api.submit_rms_norm(h, 0, dt, T, D, 1e-5, W, X, Y, ws, rs))
     ops.append(("rms_norm_fwd", b_fwd, runs))
     # --- fused RMSNorm bwd: read X, dY, dX, W, rstd; write dX; dW fp32 read-modify-write
-    b_bwd = 4 * act + D * 2 + T * 4 + 2 * D * 4
+    b_bwd = 4 * act + D * es + T * 4 + 2 * D * 4
     runs = []
     for s in range(n_sets(4 * act)):
-        X = pool.fill(act, "normal_bf16", 1)
-        W = pool.fill(D * 2, "normal_bf16", 2, 1.0, 0.02)
-        dY = pool.fill(act, "normal_bf16", 3)
+        X = pool.fill(act, fill, 1)
+        W = pool.fill(D * es, fill, 2, 1.0, 0.02)
+        dY = pool.fill(act, fill, 3)
         dX = pool.fill(act, "zeros")
         rs = pool.empty(T * 4)
         Y = pool.empty(act)
-        assert api.submit_rms_norm(h, 0, BF16, T, D, 1e-5, W, X, Y, None, rs) == 0
+        assert api.submit_rms_norm(h, 0, dt, T, D, 1e-5, W, X, Y, None, rs) == 0
         dW = pool.put(np.zeros(D, np.float32))
         runs.append(lambda X=X, W=W, dY=dY, dX=dX, rs=rs, dW=dW:
-                    api.submit_rms_norm_bwd(h, 0, BF16, BF16, T, D, 1e-5, rs, W, X, dY, dX, dW))
+                    api.submit_rms_norm_bwd(h, 0, dt, dt, T, D, 1e-5, rs, W, X, dY, dX, dW))
     ops.append(("rms_norm_bwd", b_bwd, runs))
     # --- RoPE fwd / bwd (in place): Q [T x 4096], K [T x 1024], positions t mod 2048
-    q, k = T * 4096 * 2, T * 1024 * 2
+    q, k = T * 4096 * es, T * 1024 * es
     b_rope = 2 * (q + k) + T * 4
     pos = pool.put((np.arange(T) % 2048).astype(np.int32))
     for name, fn in (("rope_fwd", api.submit_rope), ("rope_bwd", api.submit_rope_bwd_x)):
         runs = []
         for s in range(n_sets(2 * (q + k))):
-            Q = pool.fill(q, "normal_bf16", 4)
-            K = pool.fill(k, "normal_bf16", 5)
-            runs.append(lambda Q=Q, K=K, fn=fn: fn(h, 0, BF16, T * 4096, 4096, 128, 8, 500000, pos, Q, K))
+            Q = pool.fill(q, fill, 4)
+            K = pool.fill(k, fill, 5)
+            runs.append(lambda Q=Q, K=K, fn=fn: fn(h, 0, dt, T * 4096, 4096, 128, 8, 500000, pos, Q, K))
         ops.append((name, b_rope, runs))
     # --- SwiGLU fwd (3T) / bwd (5T), [T x 14336]
     F = 14336
-    t = T * F * 2
+    t = T * F * es
     runs = []
     for s in range(n_sets(3 * t)):
-        g, u, o = pool.fill(t, "normal_bf16", 6), pool.fill(t, "normal_bf16", 7), pool.empty(t)
-        runs.append(lambda g=g, u=u, o=o: api.submit_swiglu(h, 0, BF16, T, F, g, u, o))
+        g, u, o = pool.fill(t, fill, 6), pool.fill(t, fill, 7), pool.empty(t)
+        runs.append(lambda g=g, u=u, o=o: api.submit_swiglu(h, 0, dt, T, F, g, u, o))
     ops.append(("swiglu_fwd", 3 * t, runs))
     runs = []
     for s in range(n_sets(5 * t)):
-        g, u, d = pool.fill(t, "normal_bf16", 6), pool.fill(t, "normal_bf16", 7), pool.fill(t, "normal_bf16", 8)
+        g, u, d = pool.fill(t, fill, 6), pool.fill(t, fill, 7), pool.fill(t, fill, 8)
         dg, du = pool.empty(t), pool.empty(t)
-        runs.append(lambda g=g, u=u, d=d, dg=dg, du=du: api.submit_swiglu_bwd_x(h, 0, BF16, BF16, T, F, g, u, d, dg, du))
+        runs.append(lambda g=g, u=u, d=d, dg=dg, du=du: api.submit_swiglu_bwd_x(h, 0, dt, dt, T, F, g, u, d, dg, du))
     ops.append(("swiglu_bwd", 5 * t, runs))
     # --- fused softmax + cross-entropy, in place: logits [4096 x 128256]
     R, V = 4096, 128256
-    lg = R * V * 2
+    lg = R * V * es
     b_ce = 2 * lg + R * 4 + R * 4 + 4
     labels = pool.put(np.random.default_rng(9).integers(0, V, size=R).astype(np.uint32))
     runs = []
     for s in range(n_sets(2 * lg)):
-        L = pool.fill(lg, "normal_bf16", 10, 0.0, 2.0)
+        L = pool.fill(lg, fill, 10, 0.0, 2.0)
         loss, mean = pool.empty(R * 4), pool.empty(4)
-        runs.append(lambda L=L, loss=loss, mean=mean: api.submit_softmax_cross_entropy_loss(h, 0, BF16, R, V, L, labels, loss, mean))
+        runs.append(lambda L=L, loss=loss, mean=mean: api.submit_softmax_cross_entropy_loss(h, 0, dt, R, V, L, labels, loss, mean))
     ops.append(("softmax_xent_fused", b_ce, runs))
     return ops
 
@@ -651,6 +663,7 @@ def main():
     ap.add_argument("--no-head", action="store_true", help="skip the transformer-head (GEMM) line")
     ap.add_argument("--cpu-budget", type=float, default=15.0, help="seconds of CPU baseline work")
     ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--no-types", action="store_true", help="skip the fp16 and fp32 storage steps (storage_types)")
     ap.add_argument("--no-copy-reference", action="store_true",
                     help="skip timing the streaming copy of each op's byte count (copy_reference)")
     ap.add_argument("--copy-calibration", action="store_true",
@@ -674,10 +687,17 @@ def main():
         print("bench: allocating and filling rotating buffer sets", file=sys.stderr, flush=True)
         ops = build_ops(h, pool, api)
         extras = [] if args.no_extras else build_extras(h, pool, api)
+        types = {} if args.no_types else {name: build_ops(h, pool, api, dt) for name, dt in (("fp16", FP16), ("fp32", FP32))}
         h.sync()
         print("bench: timing %d steps after %d warmup" % (args.steps, args.warmup), file=sys.stderr, flush=True)
         per_op, step_ms, wall = time_ops(h, hip, ops, args.steps, args.warmup)
         per_extra = time_ops(h, hip, extras, max(5, args.steps // 2), 1)[0] if extras else {}
+        per_type = {}
+        for name, tops in types.items():
+            t_op, t_ms, _ = time_ops(h, hip, tops, max(5, args.steps // 2), 1)
+            t_bytes = sum(v["bytes"] for v in t_op.values())
+            per_type[name] = {"ms_per_step": round(t_ms, 4), "gbps": round(t_bytes / (t_ms * 1e-3) / 1e9, 1),
+                              "pct_of_peak": round(100.0 * t_bytes / (t_ms * 1e-3) / 1e9 / HBM_PEAK_GBPS, 1), "ops": t_op}
         copy_ref = None
         if not args.no_copy_reference:
             sized = dict(per_op)
@@ -714,7 +734,7 @@ def main():
                                "swiglu fwd+bwd 8192x14336, fused softmax+xent 4096x128256",
                    "tokens": 8192, "hidden": 4096, "ffn": 14336, "vocab": 128256, "ce_rows": 4096},
         "pct_of_peak": round(100.0 * value / HBM_PEAK_GBPS, 1),
-        "ops": per_op, "extras": per_extra, "copy_reference": copy_ref, "transformer_head": head,
+        "ops": per_op, "extras": per_extra, "storage_types": per_type, "copy_reference": copy_ref, "transformer_head": head,
         "host_submit_us": submit_us, "roofline": roofline,
         "cpu_baseline": cpu,
         "device": dev,

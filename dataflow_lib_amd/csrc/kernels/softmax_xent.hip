@@ -369,15 +369,27 @@ __device__ __forceinline__ void smx_regs(int n_rows, int n_cols, const T * X, TO
 	WAIT_VMEM_ALL();
 	/* Rows: each workgroup's first two are block and block + grid; every later
 	 * one is a ticket t of the launch's row counter, row 2 * grid + t. The
-	 * ticket for the row after next is taken at the top of each row (thread 0;
-	 * its reply is in well before the sum pass) and published to the other
-	 * waves with the sum reduction's barrier, so the next row's index is known
-	 * when its prefetch starts in the max pass. */
+	 * ticket for the row after next is taken at the top of each row by thread
+	 * 0, which writes that row's index to an LDS cell at once; the other waves
+	 * read it after the sum reduction's barrier, so the next row's index is
+	 * known when its prefetch starts in the max pass. The cell by row parity
+	 * was last read two rows back. Writing it at once keeps the ticket out of
+	 * the registers for the rest of the row: kept until the sum pass, it made
+	 * the fp16 fused kernel spill a prefetched chunk, whose spill waits for
+	 * every outstanding load (4096 x 128256: 412.6 -> 400.4 us; bf16 and the
+	 * softmax unchanged, outputs bit-identical). */
 	__shared__ int nextcell[2];
 	int next = row + (int) gridDim.x;
 	while (row < n_rows) {
-		unsigned ticket = 0u;
-		if (tid == 0 && next < n_rows) ticket = __hip_atomic_fetch_add(&g_smx_sched[SMX_TICKETS], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+		if (tid == 0) {
+			int r2 = n_rows;
+			if (next < n_rows) {
+				const uint32_t t = __hip_atomic_fetch_add(&g_smx_sched[SMX_TICKETS], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+				const uint32_t r = 2u * gridDim.x + t;
+				r2 = r < (uint32_t) n_rows ? (int) r : n_rows;
+			}
+			nextcell[par] = r2;
+		}
 		const __amdgpu_buffer_rsrc_t rout = make_rsrc(out + (long) row * n_cols, row_bytes);
 		/* this row: its label and the LDS part (landed: checked before the last
 		 * output pass) and the register part loaded during the last row */
@@ -524,10 +536,6 @@ __device__ __forceinline__ void smx_regs(int n_rows, int n_cols, const T * X, TO
 		}
 		float sd = sd0 + sd1;
 		float sx = SX ? so : sd;
-		if (tid == 0) {
-			const long r2 = 2L * (long) gridDim.x + (long) ticket;
-			nextcell[par] = (next < n_rows && r2 < (long) n_rows) ? (int) r2 : n_rows;
-		}
 		cells_sum2(sd, sx, sslots);
 		const int next2 = __builtin_amdgcn_readfirstlane(nextcell[par]);
 		/* y = exp(d) / sd as one exp2: exp2(d * log2(e) - log2(sd)) */
