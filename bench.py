@@ -691,10 +691,14 @@ def main():
         h.sync()
         print("bench: timing %d steps after %d warmup" % (args.steps, args.warmup), file=sys.stderr, flush=True)
         per_op, step_ms, wall = time_ops(h, hip, ops, args.steps, args.warmup)
-        per_extra = time_ops(h, hip, extras, max(5, args.steps // 2), 1)[0] if extras else {}
+        # extras and the other storage types with the same launch count per
+        # batch as their copy_reference: the two events around a batch add a
+        # few microseconds to it, which a shorter batch would charge to each
+        # launch more heavily than the copy's
+        per_extra = time_ops(h, hip, extras, args.steps, 1)[0] if extras else {}
         per_type = {}
         for name, tops in types.items():
-            t_op, t_ms, _ = time_ops(h, hip, tops, max(5, args.steps // 2), 1)
+            t_op, t_ms, _ = time_ops(h, hip, tops, args.steps, 1)
             t_bytes = sum(v["bytes"] for v in t_op.values())
             per_type[name] = {"ms_per_step": round(t_ms, 4), "gbps": round(t_bytes / (t_ms * 1e-3) / 1e9, 1),
                               "pct_of_peak": round(100.0 * t_bytes / (t_ms * 1e-3) / 1e9 / HBM_PEAK_GBPS, 1), "ops": t_op}

@@ -23,11 +23,16 @@
 #include "dtypes.h"
 #include "kernel_geometry.h"
 
-/* 16-byte chunks per lane in flight per row pass (4 KB per wave). Measured on
- * MI355X: the 2 KB K/V rows of copy_to_seq_context move in 13.7 us per
- * 8192 tokens against 14.4 us with 8 chunks; 8 KB embedding rows take the
- * same 26 us either way. A token's K and V rows are copied one after the
- * other: issuing both rows' loads before either row's stores took 14.2 us. */
+/* 16-byte chunks per lane in flight per row pass (4 KB per wave) for rows
+ * longer than 2 KB; a row of up to 2 KB is one pass of just the chunks it
+ * has (one or two per lane), so no load or store falls past its end.
+ * Measured on MI355X: the 2 KB K/V rows of copy_to_seq_context move in 13.00
+ * us per 8192 tokens with two chunks per lane against 13.16 us with four
+ * (and 14.4 us with eight); 8 KB embedding rows take the same 26 us with
+ * four or eight. A token's K and V rows are copied one after the other:
+ * issuing both rows' loads before either row's stores took 13.61 us (two
+ * chunks) and 14.2 us (four), and one wave per row instead of per token
+ * 13.42 us. */
 #define GS_CH 4
 /* Cache policy of the source rows: the embedding loads its table rows with
  * the default policy (8192 rows of a 128256 x 4096 bf16 table: 25.9 -> 23.2
@@ -44,20 +49,28 @@ template <> struct Elem<1> { typedef uint8_t t; };
 template <> struct Elem<2> { typedef uint16_t t; };
 template <> struct Elem<4> { typedef uint32_t t; };
 
+/* passes of CH 16-byte chunks per lane over a 16-byte aligned row */
+template <int CH, int LAUX>
+__device__ __forceinline__ void gs_copy_passes(const char * src, char * dst, uint32_t row_bytes, int lane) {
+	const __amdgpu_buffer_rsrc_t rs = make_rsrc(src, row_bytes);
+	const __amdgpu_buffer_rsrc_t rd = make_rsrc(dst, row_bytes);
+	for (uint32_t base = 0; base < row_bytes; base += 64u * 16u * CH) {
+		R16 v[CH];
+#pragma unroll
+		for (int i = 0; i < CH; i++) v[i] = buf_load16_aux<LAUX>(rs, (uint32_t) (lane + 64 * i) * 16u, base);
+#pragma unroll
+		for (int i = 0; i < CH; i++) buf_store16_nt(rd, (uint32_t) (lane + 64 * i) * 16u, base, v[i]);
+	}
+}
+
 /* copy one row of `row_bytes` bytes (a wave; src and dst uniform) */
 template <int ELEM, int LAUX>
 __device__ __forceinline__ void gs_copy_row(const char * src, char * dst, uint32_t row_bytes, int lane) {
 	const bool vec = ((row_bytes | (uint32_t) (uintptr_t) src | (uint32_t) (uintptr_t) dst) & 15u) == 0u;
 	if (vec) {
-		const __amdgpu_buffer_rsrc_t rs = make_rsrc(src, row_bytes);
-		const __amdgpu_buffer_rsrc_t rd = make_rsrc(dst, row_bytes);
-		for (uint32_t base = 0; base < row_bytes; base += 64u * 16u * GS_CH) {
-			R16 v[GS_CH];
-#pragma unroll
-			for (int i = 0; i < GS_CH; i++) v[i] = buf_load16_aux<LAUX>(rs, (uint32_t) (lane + 64 * i) * 16u, base);
-#pragma unroll
-			for (int i = 0; i < GS_CH; i++) buf_store16_nt(rd, (uint32_t) (lane + 64 * i) * 16u, base, v[i]);
-		}
+		if (row_bytes <= 64u * 16u) gs_copy_passes<1, LAUX>(src, dst, row_bytes, lane);
+		else if (row_bytes <= 2u * 64u * 16u) gs_copy_passes<2, LAUX>(src, dst, row_bytes, lane);
+		else gs_copy_passes<GS_CH, LAUX>(src, dst, row_bytes, lane);
 	}
 	else {
 		typedef typename Elem<ELEM>::t E;
