@@ -255,6 +255,16 @@ template <> struct SmxWord<f16_t> {
 		unpack(dw, d);
 		return dw;
 	}
+	/* the same rnd(x - m) in one packed fp16 subtraction: m is an fp16
+	 * value, and rounding the exact difference once to fp16 equals rounding
+	 * it to fp32 first (24 >= 2 * 11 + 2 bits) */
+	__device__ static __forceinline__ uint32_t diff_pk(uint32_t w, float m, float * d) {
+		const _Float16 mh = (_Float16) m;
+		const f16x2_v dv = __builtin_bit_cast(f16x2_v, w) - (f16x2_v){mh, mh};
+		d[0] = (float) dv.x;
+		d[1] = (float) dv.y;
+		return __builtin_bit_cast(uint32_t, dv);
+	}
 };
 template <> struct SmxWord<float> {
 	static constexpr int N = 1;
@@ -267,6 +277,31 @@ template <> struct SmxWord<float> {
 		return __float_as_uint(d[0]);
 	}
 };
+
+template <typename T> struct IsF16 { static constexpr bool value = false; };
+template <> struct IsF16<f16_t> { static constexpr bool value = true; };
+
+/* fp16 chunks in the max pass: the chunk's max from packed 3-input maxima
+ * (NaN-propagating like the fp32 one), and x - c in one rounding straight
+ * from the packed word's low or high half (the mixed-precision fma x * 1 - c;
+ * written out because the compiler turns fma(x, 1, c) into a conversion and
+ * a subtraction) */
+__device__ __forceinline__ float f16_chunk_max(const R16 & r, float m) {
+	const f16x2_v a = __builtin_bit_cast(f16x2_v, r.w[0]), b = __builtin_bit_cast(f16x2_v, r.w[1]);
+	const f16x2_v c = __builtin_bit_cast(f16x2_v, r.w[2]), d = __builtin_bit_cast(f16x2_v, r.w[3]);
+	const f16x2_v mx = __builtin_elementwise_maximum(__builtin_elementwise_maximum(a, b), __builtin_elementwise_maximum(c, d));
+	return __builtin_elementwise_maximum(m, __builtin_elementwise_maximum((float) mx.x, (float) mx.y));
+}
+__device__ __forceinline__ float f16_lo_minus(uint32_t w, float negc) {
+	float r;
+	__asm__("v_fma_mix_f32 %0, %1, 1.0, %2 op_sel_hi:[1,0,0]" : "=v"(r) : "v"(w), "v"(negc));
+	return r;
+}
+__device__ __forceinline__ float f16_hi_minus(uint32_t w, float negc) {
+	float r;
+	__asm__("v_fma_mix_f32 %0, %1, 1.0, %2 op_sel:[1,0,0] op_sel_hi:[1,0,0]" : "=v"(r) : "v"(w), "v"(negc));
+	return r;
+}
 
 /* Row max over one chunk. maximum() propagates NaN, so it needs no operand
  * canonicalisation and folds into 3-input max instructions; a NaN anywhere in
@@ -308,6 +343,12 @@ __device__ __forceinline__ void smx_regs(int n_rows, int n_cols, const T * X, TO
 	using W = SmxWord<T>;
 	using WO = SmxWord<TO>;
 	static_assert(sizeof(T) == sizeof(TO), "in-register output packing needs equal widths");
+	/* the fused fp16 kernel works on the packed halves where it can (fewer
+	 * conversions: fused 4096 x 128256 400.4 -> 370.0 us, outputs
+	 * bit-identical); the plain softmax, which is not held up by its
+	 * arithmetic, measured 363.2 -> 365.2 us that way and keeps the
+	 * conversions */
+	constexpr bool F16 = IsF16<T>::value && FUSED;
 	/* the loss needs sx = sum exp(x - m) over the unrounded differences and
 	 * without the label's column (fused_loss); that is not the softmax's sum,
 	 * so it is accumulated separately, for every storage type */
@@ -462,15 +503,21 @@ __device__ __forceinline__ void smx_regs(int n_rows, int n_cols, const T * X, TO
 			if (c >= SMX_PF) issue_next(c);
 			__builtin_amdgcn_sched_barrier(0);
 			if (c < nch) {
+				/* the chunk as floats (fp16: only where the label is read;
+				 * its max and terms come from the packed words) */
 				float f[VEC];
-				unpack16<T>(xr[c], f);
 				float cm = m;
+				if constexpr (F16) cm = f16_chunk_max(xr[c], m);
+				else {
+					unpack16<T>(xr[c], f);
 #pragma unroll
-				for (int e = 0; e < VEC; e++) cm = __builtin_elementwise_maximum(cm, f[e]);
+					for (int e = 0; e < VEC; e++) cm = __builtin_elementwise_maximum(cm, f[e]);
+				}
 				/* the raw labelled logit, for the loss (a workgroup-uniform
 				 * chunk test, then one thread) */
 				const bool lab_here = FUSED && c == c_lab && tid == t_lab;
 				if (lab_here) {
+					if constexpr (F16) unpack16<T>(xr[c], f);
 					float xl = f[0];
 #pragma unroll
 					for (int e = 1; e < VEC; e++)
@@ -491,7 +538,12 @@ __device__ __forceinline__ void smx_regs(int n_rows, int n_cols, const T * X, TO
 					}
 					float t[VEC];
 #pragma unroll
-					for (int e = 0; e < VEC; e++) t[e] = __builtin_amdgcn_exp2f((f[e] - mref) * SMX_LOG2E);
+					for (int e = 0; e < VEC; e++) {
+						float x_mref;
+						if constexpr (F16) x_mref = (e & 1) ? f16_hi_minus(xr[c].w[e >> 1], -mref) : f16_lo_minus(xr[c].w[e >> 1], -mref);
+						else x_mref = f[e] - mref;
+						t[e] = __builtin_amdgcn_exp2f(x_mref * SMX_LOG2E);
+					}
 					/* the loss sum leaves the label's column out (the max has
 					 * it); the terms are cleared, not f, which for fp32 is the
 					 * row itself and must stay as loaded */
@@ -524,10 +576,12 @@ __device__ __forceinline__ void smx_regs(int n_rows, int n_cols, const T * X, TO
 #pragma unroll
 				for (int i = 0; i < 4; i++) {
 					float x_m[W::N], d[W::N];
-					o.w[i] = W::diff(xr[c].w[i], m, x_m, d);
+					if constexpr (F16) o.w[i] = W::diff_pk(xr[c].w[i], m, d);
+					else o.w[i] = W::diff(xr[c].w[i], m, x_m, d);
 #pragma unroll
 					for (int e = 0; e < W::N; e++) {
-						const float ex = exp_fast(d[e]);
+						/* fp16: d * log2(e) from the packed half (mixed fma) */
+						const float ex = F16 ? __builtin_amdgcn_exp2f(fmaf(d[e], SMX_LOG2E, 0.0f)) : exp_fast(d[e]);
 						if ((i * W::N + e) & 1) sd1 += ex; else sd0 += ex;
 					}
 				}
