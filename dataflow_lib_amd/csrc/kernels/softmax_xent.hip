@@ -700,6 +700,14 @@ __device__ __forceinline__ void smx_stream_vec(int n_rows, int n_cols, const T *
 	constexpr int U = 4;
 	constexpr int VEC = VecOf<T>::N;
 	constexpr bool ROUNDS = sizeof(T) < 4;
+	/* fp32: the first HG groups of U chunks per thread (16 chunks, 256 KB of
+	 * the row per workgroup) stay in registers from the first pass to the last,
+	 * so only the rest of the row is read again (fused 4096 x 128256 fp32
+	 * 879.6 -> 787.6 us, softmax 867.9 -> 750.3 us, outputs bit-identical).
+	 * The 16-bit kernels hold none: their register budget goes to the
+	 * register-row path compiled into the same kernels, and a held group
+	 * there spilled */
+	constexpr int HG = sizeof(T) == 4 ? 4 : 0;
 	__shared__ float slots[32];
 	__shared__ float xlab_cell;
 	const int tid = threadIdx.x;
@@ -715,10 +723,7 @@ __device__ __forceinline__ void smx_stream_vec(int n_rows, int n_cols, const T *
 		const int le = (int) (lab % VEC);
 		/* pass 1: max and the online sum of exp(x - m) */
 		float m = -__builtin_inff(), mref = 0.0f, s = 0.0f;
-		for (int base = 0; base < nv; base += nt * U) {
-			R16 v[U];
-#pragma unroll
-			for (int k = 0; k < U; k++) v[k] = buf_load16(rin, (uint32_t) (base + k * nt + tid) * 16u, 0);
+		auto pass1 = [&](R16 (&v)[U], int base) {
 			float f[U][VEC];
 			float cm = m;
 #pragma unroll
@@ -761,16 +766,30 @@ __device__ __forceinline__ void smx_stream_vec(int n_rows, int n_cols, const T *
 			}
 			mref = mr;
 			m = cm;
+		};
+		R16 hold[HG > 0 ? HG : 1][U];
+		/* the held groups are read once (streaming hint), all requested
+		 * before the first is used; the rest with the default policy, so the
+		 * later passes find them in cache where they can */
+#pragma unroll
+		for (int g = 0; g < HG; g++)
+#pragma unroll
+			for (int k = 0; k < U; k++) hold[g][k] = buf_load16_nt(rin, (uint32_t) (g * nt * U + k * nt + tid) * 16u, 0);
+#pragma unroll
+		for (int g = 0; g < HG; g++)
+			if (g * nt * U < nv) pass1(hold[g], g * nt * U);
+		for (int base = HG * nt * U; base < nv; base += nt * U) {
+			R16 v[U];
+#pragma unroll
+			for (int k = 0; k < U; k++) v[k] = buf_load16(rin, (uint32_t) (base + k * nt + tid) * 16u, 0);
+			pass1(v, base);
 		}
 		const float mx = block_max(m, slots);
 		float sx = s * online_rescale(mref, mx);
 		/* pass 2 (fp16/bf16): sd = sum exp(rnd(x - mx)) */
 		float sd = 0.0f;
 		if (ROUNDS) {
-			for (int base = 0; base < nv; base += nt * U) {
-				R16 v[U];
-#pragma unroll
-				for (int k = 0; k < U; k++) v[k] = buf_load16(rin, (uint32_t) (base + k * nt + tid) * 16u, 0);
+			auto pass2 = [&](R16 (&v)[U], int base) {
 #pragma unroll
 				for (int k = 0; k < U; k++) {
 					if (base + k * nt + tid < nv) {
@@ -780,6 +799,15 @@ __device__ __forceinline__ void smx_stream_vec(int n_rows, int n_cols, const T *
 						for (int e = 0; e < VEC; e++) sd += exp_fast(rnd_in<T>(f[e] - mx));
 					}
 				}
+			};
+#pragma unroll
+			for (int g = 0; g < HG; g++)
+				if (g * nt * U < nv) pass2(hold[g], g * nt * U);
+			for (int base = HG * nt * U; base < nv; base += nt * U) {
+				R16 v[U];
+#pragma unroll
+				for (int k = 0; k < U; k++) v[k] = buf_load16(rin, (uint32_t) (base + k * nt + tid) * 16u, 0);
+				pass2(v, base);
 			}
 		}
 		__syncthreads();   /* every wave has read the max cells */
@@ -788,10 +816,7 @@ __device__ __forceinline__ void smx_stream_vec(int n_rows, int n_cols, const T *
 		if (!ROUNDS) sd = sx + (lab_ok ? __builtin_amdgcn_exp2f((xlab_cell - mx) * SMX_LOG2E) : 0.0f);
 		const float nlog2s = -__builtin_amdgcn_logf(sd);
 		/* last pass: y = exp(rnd(x - mx)) / sd */
-		for (int base = 0; base < nv; base += nt * U) {
-			R16 v[U];
-#pragma unroll
-			for (int k = 0; k < U; k++) v[k] = buf_load16_nt(rin, (uint32_t) (base + k * nt + tid) * 16u, 0);
+		auto pass3 = [&](R16 (&v)[U], int base) {
 #pragma unroll
 			for (int k = 0; k < U; k++) {
 				const int c = base + k * nt + tid;
@@ -807,6 +832,15 @@ __device__ __forceinline__ void smx_stream_vec(int n_rows, int n_cols, const T *
 				}
 				buf_store16_nt(rout, (uint32_t) c * 16u, 0, o);
 			}
+		};
+#pragma unroll
+		for (int g = 0; g < HG; g++)
+			if (g * nt * U < nv) pass3(hold[g], g * nt * U);
+		for (int base = HG * nt * U; base < nv; base += nt * U) {
+			R16 v[U];
+#pragma unroll
+			for (int k = 0; k < U; k++) v[k] = buf_load16_nt(rin, (uint32_t) (base + k * nt + tid) * 16u, 0);
+			pass3(v, base);
 		}
 		if (FUSED && tid == 0 && loss) store_loss(loss, row, lab_ok ? fused_loss(sx, mx, xlab_cell) : __builtin_nanf(""));
 		__syncthreads();   /* the cells are rewritten for the next row */
