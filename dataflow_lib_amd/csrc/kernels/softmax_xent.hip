@@ -700,14 +700,18 @@ __device__ __forceinline__ void smx_stream_vec(int n_rows, int n_cols, const T *
 	constexpr int U = 4;
 	constexpr int VEC = VecOf<T>::N;
 	constexpr bool ROUNDS = sizeof(T) < 4;
-	/* fp32: the first HG groups of U chunks per thread (16 chunks, 256 KB of
-	 * the row per workgroup) stay in registers from the first pass to the last,
-	 * so only the rest of the row is read again (fused 4096 x 128256 fp32
-	 * 879.6 -> 787.6 us, softmax 867.9 -> 750.3 us, outputs bit-identical).
-	 * The 16-bit kernels hold none: their register budget goes to the
-	 * register-row path compiled into the same kernels, and a held group
-	 * there spilled */
-	constexpr int HG = sizeof(T) == 4 ? 4 : 0;
+	/* The first HG groups of UH chunks per thread stay in registers from the
+	 * first pass to the last, so only the rest of the row is read again:
+	 * fp32 16 chunks (256 KB of the row per workgroup; fused 4096 x 128256
+	 * 879.6 -> 787.6 us, softmax 867.9 -> 750.3 us), 16-bit rows 8 chunks in
+	 * the softmax and 6 in the fused kernel, whose label and loss state leave
+	 * fewer registers (8 spilled there); held groups of two chunks, so the
+	 * first pass's working set stays small (4096 x 151936: bf16 fused 660.9
+	 * -> 591.1 us, softmax 651.1 -> 563.5 us, fp16 665.1 -> 588.5 and 654.3
+	 * -> 559.8 us). The outputs are bit-identical; the loss sum is rescaled
+	 * at other chunks, so a loss can differ in its last bits. */
+	constexpr int HG = sizeof(T) == 4 ? 4 : (FUSED ? 3 : 4);
+	constexpr int UH = sizeof(T) == 4 ? U : 2;   /* chunks per held group */
 	__shared__ float slots[32];
 	__shared__ float xlab_cell;
 	const int tid = threadIdx.x;
@@ -723,7 +727,8 @@ __device__ __forceinline__ void smx_stream_vec(int n_rows, int n_cols, const T *
 		const int le = (int) (lab % VEC);
 		/* pass 1: max and the online sum of exp(x - m) */
 		float m = -__builtin_inff(), mref = 0.0f, s = 0.0f;
-		auto pass1 = [&](R16 (&v)[U], int base) {
+		auto pass1 = [&](auto & v, int base) {
+			constexpr int U = sizeof(v) / sizeof(R16);
 			float f[U][VEC];
 			float cm = m;
 #pragma unroll
@@ -767,18 +772,18 @@ __device__ __forceinline__ void smx_stream_vec(int n_rows, int n_cols, const T *
 			mref = mr;
 			m = cm;
 		};
-		R16 hold[HG > 0 ? HG : 1][U];
+		R16 hold[HG][UH];
 		/* the held groups are read once (streaming hint), all requested
 		 * before the first is used; the rest with the default policy, so the
 		 * later passes find them in cache where they can */
 #pragma unroll
 		for (int g = 0; g < HG; g++)
 #pragma unroll
-			for (int k = 0; k < U; k++) hold[g][k] = buf_load16_nt(rin, (uint32_t) (g * nt * U + k * nt + tid) * 16u, 0);
+			for (int k = 0; k < UH; k++) hold[g][k] = buf_load16_nt(rin, (uint32_t) (g * nt * UH + k * nt + tid) * 16u, 0);
 #pragma unroll
 		for (int g = 0; g < HG; g++)
-			if (g * nt * U < nv) pass1(hold[g], g * nt * U);
-		for (int base = HG * nt * U; base < nv; base += nt * U) {
+			if (g * nt * UH < nv) pass1(hold[g], g * nt * UH);
+		for (int base = HG * nt * UH; base < nv; base += nt * U) {
 			R16 v[U];
 #pragma unroll
 			for (int k = 0; k < U; k++) v[k] = buf_load16(rin, (uint32_t) (base + k * nt + tid) * 16u, 0);
@@ -789,7 +794,8 @@ __device__ __forceinline__ void smx_stream_vec(int n_rows, int n_cols, const T *
 		/* pass 2 (fp16/bf16): sd = sum exp(rnd(x - mx)) */
 		float sd = 0.0f;
 		if (ROUNDS) {
-			auto pass2 = [&](R16 (&v)[U], int base) {
+			auto pass2 = [&](auto & v, int base) {
+				constexpr int U = sizeof(v) / sizeof(R16);
 #pragma unroll
 				for (int k = 0; k < U; k++) {
 					if (base + k * nt + tid < nv) {
@@ -802,8 +808,8 @@ __device__ __forceinline__ void smx_stream_vec(int n_rows, int n_cols, const T *
 			};
 #pragma unroll
 			for (int g = 0; g < HG; g++)
-				if (g * nt * U < nv) pass2(hold[g], g * nt * U);
-			for (int base = HG * nt * U; base < nv; base += nt * U) {
+				if (g * nt * UH < nv) pass2(hold[g], g * nt * UH);
+			for (int base = HG * nt * UH; base < nv; base += nt * U) {
 				R16 v[U];
 #pragma unroll
 				for (int k = 0; k < U; k++) v[k] = buf_load16(rin, (uint32_t) (base + k * nt + tid) * 16u, 0);
@@ -816,7 +822,8 @@ __device__ __forceinline__ void smx_stream_vec(int n_rows, int n_cols, const T *
 		if (!ROUNDS) sd = sx + (lab_ok ? __builtin_amdgcn_exp2f((xlab_cell - mx) * SMX_LOG2E) : 0.0f);
 		const float nlog2s = -__builtin_amdgcn_logf(sd);
 		/* last pass: y = exp(rnd(x - mx)) / sd */
-		auto pass3 = [&](R16 (&v)[U], int base) {
+		auto pass3 = [&](auto & v, int base) {
+			constexpr int U = sizeof(v) / sizeof(R16);
 #pragma unroll
 			for (int k = 0; k < U; k++) {
 				const int c = base + k * nt + tid;
@@ -835,8 +842,8 @@ __device__ __forceinline__ void smx_stream_vec(int n_rows, int n_cols, const T *
 		};
 #pragma unroll
 		for (int g = 0; g < HG; g++)
-			if (g * nt * U < nv) pass3(hold[g], g * nt * U);
-		for (int base = HG * nt * U; base < nv; base += nt * U) {
+			if (g * nt * UH < nv) pass3(hold[g], g * nt * UH);
+		for (int base = HG * nt * UH; base < nv; base += nt * U) {
 			R16 v[U];
 #pragma unroll
 			for (int k = 0; k < U; k++) v[k] = buf_load16_nt(rin, (uint32_t) (base + k * nt + tid) * 16u, 0);
