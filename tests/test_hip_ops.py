@@ -640,6 +640,10 @@ def test_swiglu_unaligned(hdl):
 # ---------------- softmax / cross-entropy ----------------
 
 SMX_SHAPES = [(4, 128256), (3, 1000), (2, 1001), (2, 140000), (5, 64), (1, 1)]
+# rows just past the register path (16-bit: 131,072 columns, fp32: 65,536),
+# where one thread holds one chunk more than the others, and a row of 32
+# (16-bit) or 64 (fp32) chunks per thread, of which the first 6-16 are held
+SMX_SHAPES += [(5, 131080), (4, 65540), (3, 262144)]
 SMX_SHAPES += [(_ri(1, 40), _ri(1, 150000)), (_ri(1, 40), 8 * _ri(1, 16384))]
 
 
