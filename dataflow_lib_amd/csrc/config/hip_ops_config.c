@@ -340,13 +340,13 @@ int swiglu_bwd_x_set_launch_config(Hip_Launch_Config * hip_launch_config, Datafl
 
 /* ---------------- softmax / cross-entropy ---------------- */
 
-/* The 16-bit and fp32 softmax kernels (softmax_xent.hip) hand rows out from a
- * counter in the code object and count finished workgroups there, so the
- * handle orders them across its streams; the fp8 softmax (fp8_ops.hip) keeps
- * no launch-wide state. */
+/* The softmax kernels (softmax_xent.hip, and the fp8 softmax in fp8_ops.hip
+ * on its long-row path) hand rows out from a counter in the code object and
+ * count finished workgroups there, so the handle orders them across its
+ * streams. */
 int softmax_set_attribute_config(Dataflow_Handle * dataflow_handle, Hip_Function * hip_function) {
 	(void) dataflow_handle;
-	hip_function->function_config.shares_module_scratch = !is_fp8(hip_function, 2);
+	hip_function->function_config.shares_module_scratch = 1;
 	return 0;
 }
 

@@ -336,7 +336,13 @@ __device__ __forceinline__ void softmax_fp8_regs(int n_rows, int n_cols, const T
  * 64 KB, so the two-workgroup register path of shorter rows, compiled into the
  * same kernel, still fits two workgroups per CU. Pieces past the row end load
  * zeros and are left out of the max and the sum; their stores fall outside
- * the row's range and store nothing. */
+ * the row's range and store nothing. Rows are handed out as workgroups free
+ * up, as in the 16-bit softmax: each workgroup's first two rows are block and
+ * block + grid, every later one a ticket of the code object's launch-wide row
+ * counter (g_smx_sched), taken by thread 0 at the top of a row for the row
+ * after next and written to an LDS cell at once; the max reduction's barrier
+ * publishes it before the next row is requested. The caller resets the
+ * counter at the end of the launch (smx_launch_end). */
 template <typename TF, typename TO>
 __device__ __forceinline__ void softmax_fp8_pf(int n_rows, int n_cols, const TF * X, TO * out) {
 	constexpr int nt = SMX_THREADS;
@@ -347,6 +353,7 @@ __device__ __forceinline__ void softmax_fp8_pf(int n_rows, int n_cols, const TF 
 	__shared__ __attribute__((aligned(16))) float mslots[SMX_WAVES];
 	__shared__ __attribute__((aligned(16))) float sslots[2 * SMX_WAVES];
 	__shared__ __attribute__((aligned(16))) uint8_t pf[NL * nt * 16];
+	__shared__ int nextcell;
 	const int np = n_cols / 8;
 	const int tid = (int) threadIdx.x;
 	const int wave_base = tid & ~63;
@@ -366,10 +373,20 @@ __device__ __forceinline__ void softmax_fp8_pf(int n_rows, int n_cols, const TF 
 		}
 	};
 	int row = blockIdx.x;
+	int next = row + (int) gridDim.x;
 	if (row < n_rows) request(row);
 	vmem_wait_all();
 	cells_barrier();
-	for (; row < n_rows; row += gridDim.x) {
+	while (row < n_rows) {
+		/* the ticket for the row after next, requested here and read after
+		 * the max pass, so that thread 0 waits for its return (and, since
+		 * vector-memory operations complete in order, for the previous row's
+		 * stores) only there. An atomic increment with no wrap-around, which
+		 * the compiler's atomic optimizer leaves alone: an atomic add gets
+		 * its result broadcast, and so waited for, right where it is made. */
+		unsigned tk = 0u;
+		if (tid == 0 && next < n_rows)
+			tk = __builtin_amdgcn_atomic_inc32(&g_smx_sched[SMX_TICKETS], 0xffffffffu, __ATOMIC_RELAXED, "agent");
 		R8 cur[NP];
 #pragma unroll
 		for (int j = 0; j < NH; j++) cur[j] = *reinterpret_cast<const R8 *>(&pf[8 * (tid + nt * j)]);
@@ -386,10 +403,17 @@ __device__ __forceinline__ void softmax_fp8_pf(int n_rows, int n_cols, const TF 
 				for (int e = 0; e < 8; e++) m = __builtin_elementwise_maximum(m, f[e]);
 			}
 		}
+		/* the row after next (n_rows: none); every wave reads the cell after
+		 * this row's max reduction, before the barrier at the row's end lets
+		 * thread 0 write it again */
+		if (tid == 0) {
+			const unsigned r = 2u * gridDim.x + tk;
+			nextcell = (next < n_rows && r < (unsigned) n_rows) ? (int) r : n_rows;
+		}
 		m = cells_max(m, mslots);
+		const int next2 = __builtin_amdgcn_readfirstlane(nextcell);
 		/* every wave has read its pieces (each waited for its LDS reads
 		 * before the barrier in cells_max): the buffer takes the next row */
-		const int next = row + (int) gridDim.x;
 		if (next < n_rows) request(next);
 #pragma unroll
 		for (int j = 0; j < NP; j++) reg_barrier8(cur[j]);
@@ -421,6 +445,8 @@ __device__ __forceinline__ void softmax_fp8_pf(int n_rows, int n_cols, const TF 
 		 * landed; the barrier then waits for every wave's */
 		__builtin_amdgcn_s_waitcnt(0x4F70);   /* vmcnt(16) */
 		cells_barrier();
+		row = next;
+		next = next2;
 	}
 	vmem_wait_all();
 }
@@ -434,6 +460,7 @@ __device__ __forceinline__ void softmax_fp8(int n_rows, int n_cols, const TF * X
 	__shared__ float slots[32];
 	if (blockDim.x == SMX_THREADS && f8_smx_pf_ok(n_cols) && aligned16(X) && aligned16(out)) {
 		softmax_fp8_pf<TF, TO>(n_rows, n_cols, X, out);
+		smx_launch_end<false>(n_rows, nullptr, nullptr);
 		return;
 	}
 	if (blockDim.x == F8_SMX_THREADS && f8_smx_regs_ok(n_cols) && aligned16(X) && aligned16(out)) {

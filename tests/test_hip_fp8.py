@@ -379,6 +379,42 @@ def test_softmax_fp8_special_rows(hdl, fb, shape):
     assert np.isnan(to_f64(out, bdt)[n_rows - 3]).all()
 
 
+def test_softmax_fp8_on_two_streams_matches_one_stream(hdl):
+    """The fp8 softmax's long-row path hands rows out from the same counter in
+    the code object as the 16-bit fused loss op (and counts finished
+    workgroups there), so the handle orders the two across its streams: the
+    two ops alternating between streams without waits, with more rows than
+    two per workgroup so that both take tickets, give the same bits as the
+    same launches on one stream, and the fp8 probabilities match the oracle."""
+    from dataflow_lib_amd import api
+    from test_hip_ops import logits
+    fdt, bdt = FP8E4M3, BF16
+    ce_shape, sm_shape = (600, 32000), (600, 65552)
+    Xc = logits(BF16, ce_shape, seed=160)
+    lab = rng(161).integers(0, ce_shape[1], size=ce_shape[0]).astype(np.uint32)
+    Xs = to_storage(normal(162, sm_shape, std=2.0), fdt)
+    outs = []
+    for two_streams in (False, True):
+        with Dev(hdl) as d:
+            pc, pl, ploss, pmean = d.put(Xc), d.put(lab), d.empty(4 * ce_shape[0]), d.empty(4)
+            ps, po = d.put(Xs), d.empty(2 * Xs.size)
+            hdl.sync()
+            for rnd in range(3):
+                if rnd > 0:
+                    hdl.sync()
+                    hdl.to_device(np.ascontiguousarray(Xc), pc)   # fresh logits (the loss op works in place)
+                assert api.submit_softmax_cross_entropy_loss(hdl, 0, BF16, ce_shape[0], ce_shape[1], pc, pl, ploss, pmean) == 0
+                assert api.submit_softmax(hdl, 1 if two_streams else 0, fdt, bdt, sm_shape[0], sm_shape[1], ps, po) == 0
+            hdl.sync()
+            outs.append([d.get(pc, ce_shape, np.uint16), d.get(ploss, (ce_shape[0],), np.float32),
+                         d.get(pmean, (1,), np.float32), d.get(po, sm_shape, NP_STORAGE[bdt])])
+    for r, g in zip(outs[0], outs[1]):
+        assert np.array_equal(r.view(np.uint8), g.view(np.uint8))
+    pre = np.empty(sm_shape)
+    assert oracle().oracle_softmax(fdt, bdt, sm_shape[0], sm_shape[1], ptr(Xs), ptr(pre)) == 0
+    check_rounded(outs[1][3], bdt, pre, what="softmax fp8 on two streams")
+
+
 @pytest.mark.parametrize("fb", [(FP8E4M3, BF16), (FP8E5M2, FP16)], ids=["e4m3_bf16", "e5m2_fp16"])
 def test_rms_norm_bwd_w_fp8_on_two_streams_matches_one_stream(hdl, fb):
     """The fp8 dW ops keep their partial rows in the same module scratch as the
