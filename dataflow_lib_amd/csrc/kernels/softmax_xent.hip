@@ -282,12 +282,25 @@ template <typename T> struct IsF16 { static constexpr bool value = false; };
 template <> struct IsF16<f16_t> { static constexpr bool value = true; };
 
 /* fp16 chunks in the max pass: the chunk's max from packed 3-input maxima
- * (NaN-propagating like the fp32 one) */
+ * (NaN-propagating like the fp32 one), and x - c in one rounding straight
+ * from the packed word's low or high half (the mixed-precision fma x * 1 - c;
+ * written out because the compiler turns fma(x, 1, c) into a conversion and
+ * a subtraction) */
 __device__ __forceinline__ float f16_chunk_max(const R16 & r, float m) {
 	const f16x2_v a = __builtin_bit_cast(f16x2_v, r.w[0]), b = __builtin_bit_cast(f16x2_v, r.w[1]);
 	const f16x2_v c = __builtin_bit_cast(f16x2_v, r.w[2]), d = __builtin_bit_cast(f16x2_v, r.w[3]);
 	const f16x2_v mx = __builtin_elementwise_maximum(__builtin_elementwise_maximum(a, b), __builtin_elementwise_maximum(c, d));
 	return __builtin_elementwise_maximum(m, __builtin_elementwise_maximum((float) mx.x, (float) mx.y));
+}
+__device__ __forceinline__ float f16_lo_minus(uint32_t w, float negc) {
+	float r;
+	__asm__("v_fma_mix_f32 %0, %1, 1.0, %2 op_sel_hi:[1,0,0]" : "=v"(r) : "v"(w), "v"(negc));
+	return r;
+}
+__device__ __forceinline__ float f16_hi_minus(uint32_t w, float negc) {
+	float r;
+	__asm__("v_fma_mix_f32 %0, %1, 1.0, %2 op_sel:[1,0,0] op_sel_hi:[1,0,0]" : "=v"(r) : "v"(w), "v"(negc));
+	return r;
 }
 
 /* Row max over one chunk. maximum() propagates NaN, so it needs no operand
@@ -475,22 +488,16 @@ __device__ __forceinline__ void smx_regs(int n_rows, int n_cols, const T * X, TO
 		 * passes). Each request sits just before this row's chunk c is used
 		 * (the scheduling barrier keeps that order), so the waves compute
 		 * while the memory pipeline accepts them. For the loss, sx is summed
-		 * in the same pass online: so = sum 2^(x log2e - cref) against a
-		 * reference cref = mref log2e, where mref trails the running max by
-		 * at most 64, rescaled when it moves. Keeping the reference in the
-		 * log2 domain makes each term one fma and one exp2 (measured
-		 * 383.1 -> 379.8 us against x - mref, then the scaling).
+		 * in the same pass online: so = sum exp(x - mref) against a reference
+		 * that trails the running max by at most 64, rescaled when it moves.
 		 * (Summing it in the sum pass instead, from exp(d) corrected
 		 * for the rounding of x - m, measured 7 us faster to first order but
 		 * misses the 1e-4 loss bound on confident rows, and 28 us slower to
 		 * second order: that pass is already the kernel's busiest.) */
 		float m = -__builtin_inff();
-		/* cref: the online sum's reference (log2 domain), a placeholder 0
-		 * until the lane has seen a finite value; mref64 = mref + 64, -inf
-		 * until then. Moving cref clamps the exponent at 0 so that a first
-		 * max below -88 multiplies the empty sum by 1, not by an overflowed
-		 * exp2 (0 * inf would make it NaN). */
-		float cref = 0.0f, mref64 = -__builtin_inff(), so = 0.0f;
+		/* mref: the online sum's reference, a placeholder 0 until the lane
+		 * has seen a finite value; mref64 = mref + 64, -inf until then */
+		float mref = 0.0f, mref64 = -__builtin_inff(), so = 0.0f;
 #pragma unroll
 		for (int c = 0; c < SMX_MAXCH; c++) {
 			if (c >= SMX_PF) issue_next(c);
@@ -525,21 +532,17 @@ __device__ __forceinline__ void smx_regs(int n_rows, int n_cols, const T * X, TO
 					 * against moving it every chunk */
 					const bool move = cm > mref64;
 					if (__builtin_amdgcn_ballot_w64(move)) {
-						const float cnew = cm * SMX_LOG2E;
-						so = move ? so * __builtin_amdgcn_exp2f(fminf(cref - cnew, 0.0f)) : so;
-						cref = move ? cnew : cref;
+						so = move ? so * online_rescale(mref, cm) : so;
+						mref = move ? cm : mref;
 						mref64 = move ? cm + 64.0f : mref64;
 					}
 					float t[VEC];
 #pragma unroll
 					for (int e = 0; e < VEC; e++) {
-						float x;
-						if constexpr (F16) {
-							const f16x2_v h = __builtin_bit_cast(f16x2_v, xr[c].w[e >> 1]);
-							x = (e & 1) ? (float) h.y : (float) h.x;
-						}
-						else x = f[e];
-						t[e] = __builtin_amdgcn_exp2f(fmaf(x, SMX_LOG2E, -cref));
+						float x_mref;
+						if constexpr (F16) x_mref = (e & 1) ? f16_hi_minus(xr[c].w[e >> 1], -mref) : f16_lo_minus(xr[c].w[e >> 1], -mref);
+						else x_mref = f[e] - mref;
+						t[e] = __builtin_amdgcn_exp2f(x_mref * SMX_LOG2E);
 					}
 					/* the loss sum leaves the label's column out (the max has
 					 * it); the terms are cleared, not f, which for fp32 is the
@@ -556,7 +559,7 @@ __device__ __forceinline__ void smx_regs(int n_rows, int n_cols, const T * X, TO
 			}
 		}
 		m = cells_max(m, mslots);
-		if (SX) so *= __builtin_amdgcn_exp2f(fminf(-fmaf(m, SMX_LOG2E, -cref), 0.0f));   /* sx against the row max */
+		if (SX) so *= online_rescale(mref, m);   /* sx against the row max */
 #pragma unroll
 		for (int c = 0; c < SMX_MAXCH; c++) reg_barrier(xr[c]);
 

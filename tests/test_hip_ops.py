@@ -837,6 +837,43 @@ def test_fused_loss_on_shifted_rows(hdl, dt, shape):
 
 
 @pytest.mark.parametrize("dt", DTS, ids=dt_id)
+@pytest.mark.parametrize("case", [(16, 1.0, -1.0e4), (16, 1.0, 1.0e4), (1000, 10.0, -1.0e4), (1000, 10.0, 1.0e4)],
+                         ids=lambda c: "%dcols_std%g_shift%g" % c)
+def test_fused_loss_on_short_rows_far_from_zero(hdl, dt, case):
+    """Short rows of logits near +-1e4 on the register path (600 rows, so
+    workgroups take tickets), the label holding the row max by one step of
+    the storage type there (8 in fp32 and fp16, 64 in bf16), so the losses
+    are about the sum of the other columns' exp(x - x_label), small numbers
+    whose relative precision rests on that sum. It is taken against a
+    reference that trails the row max; a rounding of that reference that is
+    not cancelled exactly shows as a relative error up to ~3e-4 at |x| = 1e4
+    (an fp32 ulp of x log2(e)): a form of the kernel that kept the reference
+    in the log2 domain and clamped the final rescale's exponent at 0 failed
+    here on about a third of the rows."""
+    from dataflow_lib_amd import api
+    n_cols, std, shift = case
+    shape = (600, n_cols)
+    x = to_f64(to_storage(normal(791, shape, std=std) + shift, dt), dt)
+    labels = rng(792).integers(0, n_cols, size=shape[0]).astype(np.uint32)
+    step = 64.0 if dt == BF16 else 8.0
+    x[np.arange(shape[0]), labels] = x.max(axis=1) + step
+    X = to_storage(x, dt)
+    lo, hi, loss, mean = np.empty(shape), np.empty(shape), np.empty(shape[0]), np.zeros(1)
+    assert oracle().oracle_softmax_cross_entropy(dt, shape[0], n_cols, ptr(X), ptr(labels), ptr(lo), ptr(hi),
+                                                 ptr(loss), ptr(mean)) == 0
+    assert np.isfinite(loss).all() and (loss > 1e-30).all() and np.median(loss) < 0.1
+    with Dev(hdl) as d:
+        px, pl, ploss, pmean = d.put(X), d.put(labels), d.empty(4 * shape[0]), d.empty(4)
+        assert api.submit_softmax_cross_entropy_loss(hdl, 0, dt, shape[0], n_cols, px, pl, ploss, pmean) == 0
+        out = d.get(px, shape, NP_STORAGE[dt])
+        gl = d.get(ploss, (shape[0],), np.float32)
+        gm = d.get(pmean, (1,), np.float32)
+    check_rounded(out, dt, lo, hi, what="fused dlogits, short rows far from zero")
+    check_f32(gl, loss, rel=1e-4, what="fused loss, short rows far from zero")
+    check_f32(gm, mean, rel=1e-4, what="fused mean loss, short rows far from zero")
+
+
+@pytest.mark.parametrize("dt", DTS, ids=dt_id)
 @pytest.mark.parametrize("shape", SHIFTED_SHAPES, ids=lambda s: "%dx%d" % s)
 def test_fused_loss_keeps_small_losses(hdl, dt, shape):
     """Rows the label wins by 5 to 40 over a N(0, 1) bulk, so each loss is
