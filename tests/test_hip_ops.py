@@ -645,6 +645,10 @@ SMX_SHAPES = [(4, 128256), (3, 1000), (2, 1001), (2, 140000), (5, 64), (1, 1)]
 # (16-bit) or 64 (fp32) chunks per thread, of which the first 6-16 are held
 SMX_SHAPES += [(5, 131080), (4, 65540), (3, 262144)]
 SMX_SHAPES += [(_ri(1, 40), _ri(1, 150000)), (_ri(1, 40), 8 * _ri(1, 16384))]
+# long rows on the streaming path with more rows than workgroups, so rows past
+# each workgroup's first are handed out by ticket (600 x 140,000: every type
+# streams; 16-bit rows of 70,000 stay on the register path)
+SMX_SHAPES += [(600, 140000)]
 
 
 def logits(dt, shape, seed=101):
